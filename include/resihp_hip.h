@@ -1,0 +1,257 @@
+/*
+ * resihp_hip.h -- C ABI of the MI355X (gfx950) kernels behind the decoder-LM
+ * forward/backward step of resihp/model.py and the shard math of
+ * resihp/parallel/tp.py, plus the on-device TP re-slice of
+ * resihp/parallel/reshard.py.
+ *
+ * Conventions shared by every entry point:
+ *   - plain device pointers, element counts and leading dimensions in
+ *     ELEMENTS (not bytes) unless a name says *_bytes;
+ *   - `stream` is a hipStream_t passed as void*; work is only enqueued, no
+ *     entry point synchronises the device or allocates device memory;
+ *   - scratch space comes from the caller (`workspace`, sized by the matching
+ *     *_workspace_bytes query);
+ *   - return value 0 = success; otherwise an RH_ERR_* code and a message
+ *     available from rh_last_error() (thread-local).
+ *
+ * Storage dtypes: RH_DTYPE_F32 (IEEE fp32) and RH_DTYPE_BF16 (bfloat16,
+ * round-to-nearest-even).  Every kernel accumulates in fp32.
+ *
+ * The reference (ksqbxm/resihp-reproduction) is pure Python on PyTorch; it has
+ * no foreign-function interface of its own.  Each entry point below names the
+ * reference call site(s) whose ATen op it replaces.
+ */
+#ifndef RESIHP_HIP_H
+#define RESIHP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status / dtype codes ------------------------------------------------ */
+#define RH_OK 0
+#define RH_ERR_INVALID 1     /* bad shape / pointer / argument (maps to ValueError) */
+#define RH_ERR_HIP 2         /* HIP runtime or launch failure                       */
+#define RH_ERR_UNSUPPORTED 3 /* valid request this build does not implement         */
+
+#define RH_DTYPE_F32 0
+#define RH_DTYPE_BF16 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int rh_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* rh_last_error(void);
+
+/* ---- GEMM ------------------------------------------------------------------
+ * Replaces F.linear / nn.Linear (bias-free, weight [out,in]) and the matmuls of
+ * its autograd backward:
+ *   q/k/v projections   resihp/model.py:55-57,63-65   resihp/parallel/tp.py:235-237
+ *   out_proj            resihp/model.py:58,71         resihp/parallel/tp.py:243
+ *   fc1 / fc2           resihp/model.py:77-78,81      resihp/parallel/tp.py:247-248
+ *   lm_head             resihp/model.py:116,133       resihp/parallel/tp.py:272
+ * All matrices are row-major.  Layouts:
+ *   RH_GEMM_NT : D[M,N] = A[M,K] . B[N,K]^T   (forward  y  = x . W^T)
+ *   RH_GEMM_NN : D[M,N] = A[M,K] . B[K,N]     (dgrad    dx = dy . W)
+ *   RH_GEMM_TN : D[M,N] = A[K,M]^T . B[K,N]   (wgrad    dW = dy^T . x)
+ * then  v = alpha*acc + beta*C  and the epilogue:
+ *   RH_EPI_NONE      D = v
+ *   RH_EPI_GELU      aux_out = v, D = gelu(v)            (fc1 + exact-erf GELU,
+ *                                                       model.py:81, tp.py:247)
+ *   RH_EPI_GELU_GRAD D = v * gelu'(aux)                  (GELU backward fused
+ *                                                       into the fc2 dgrad)
+ * Segmented operands let three separate q/k/v weights act as one [3*d_l, d]
+ * matrix without a copy: row r of the *stored* B lives at
+ * B[r / b_seg_rows] + (r % b_seg_rows)*ldb, and row m of D lives at
+ * D[m / d_seg_rows] + (m % d_seg_rows)*ldd.  With b_nseg == 1 (d_nseg == 1)
+ * only B[0] (D[0]) is used.  C == NULL with beta != 0 reads C from D
+ * (in-place accumulation, e.g. into a parameter's .grad).
+ */
+#define RH_GEMM_NT 0
+#define RH_GEMM_NN 1
+#define RH_GEMM_TN 2
+
+#define RH_EPI_NONE 0
+#define RH_EPI_GELU 1
+#define RH_EPI_GELU_GRAD 2
+
+#define RH_MAX_SEG 4
+
+typedef struct rh_gemm_desc {
+  int32_t dtype;
+  int32_t layout;
+  int32_t epilogue;
+  int32_t b_nseg;
+  int32_t d_nseg;
+  int32_t reserved;
+  int64_t M, N, K;
+  const void* A;
+  int64_t lda;
+  const void* B[RH_MAX_SEG];
+  int64_t ldb;
+  int64_t b_seg_rows;
+  float alpha;
+  float beta;
+  const void* C;
+  int64_t ldc;
+  void* D[RH_MAX_SEG];
+  int64_t ldd;
+  int64_t d_seg_rows;
+  const void* aux;
+  void* aux_out;
+  int64_t ldaux;
+} rh_gemm_desc;
+
+/* Workspace (bytes) rh_gemm would use for split-K on this device; 0 if none. */
+int rh_gemm_workspace_bytes(const rh_gemm_desc* desc, int64_t* bytes);
+/* A smaller workspace than requested is legal: the call then runs unsplit. */
+int rh_gemm(const rh_gemm_desc* desc, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- causal self-attention core ---------------------------------------------
+ * Replaces  scores = q @ k^T / sqrt(Dh); masked_fill(triu(ones,1), -inf);
+ * softmax(-1); @ v   (resihp/model.py:62-70, resihp/parallel/tp.py:231-242)
+ * and its autograd backward, as one fused online-softmax kernel that never
+ * materialises the [S,S] scores.
+ * Token t = b*seq + s; element (t, head h, d) of q/k/v/o/do/dq/dk/dv is at
+ * ptr + t*ld + h*head_dim + d.  lse is [batch, heads, seq] fp32, natural log of
+ * the softmax denominator of each query row (saved by forward for backward).
+ * `causal` = 1 masks keys after the query (the diagonal is kept), as the
+ * reference always does; 0 attends to every key.
+ */
+int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                const void* q, const void* k, const void* v, int64_t ld_qkv,
+                void* o, int64_t ld_o, float* lse, float scale, int causal, void* stream);
+int rh_attn_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t heads, int64_t* bytes);
+int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                const void* q, const void* k, const void* v, int64_t ld_qkv,
+                const void* o, int64_t ld_o, const void* dout, int64_t ld_do, const float* lse,
+                void* dq, void* dk, void* dv, int64_t ld_dqkv, float scale, int causal,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- LayerNorm ----------------------------------------------------------------
+ * Replaces nn.LayerNorm / F.layer_norm over the last dim, eps default 1e-5,
+ * biased variance (resihp/model.py:89,91,95-96,115,132;
+ * resihp/parallel/tp.py:262,264,268) and its backward.  x/y/dy/dx are
+ * [rows, dim] contiguous; gamma/beta [dim]; mean/rstd [rows] fp32.
+ * Backward: dx = LN_bwd(dy) (+ dresidual when non-NULL: the residual-branch
+ * gradient of x + sublayer(LN(x)), model.py:95-96, fused here);
+ * dgamma/dbeta (either may be NULL) are written, or added to when
+ * accumulate != 0 (gradient accumulation into .grad).
+ */
+int rh_layernorm_fwd(int dtype, int64_t rows, int64_t dim, const void* x, const void* gamma,
+                     const void* beta, float eps, void* y, float* mean, float* rstd, void* stream);
+int rh_layernorm_bwd_workspace_bytes(int64_t rows, int64_t dim, int64_t* bytes);
+int rh_layernorm_bwd(int dtype, int64_t rows, int64_t dim, const void* dy, const void* x,
+                     const float* mean, const float* rstd, const void* gamma,
+                     const void* dresidual, void* dx, void* dgamma, void* dbeta, int accumulate,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- elementwise ----------------------------------------------------------------
+ * rh_gelu_fwd/bwd : F.gelu, approximate='none' (model.py:81, tp.py:247).
+ * rh_add          : out = a + b, the residual add x + sublayer(.)
+ *                   (model.py:95-96, tp.py:263,265) when not fused.
+ * rh_scale_by     : x[r, c] *= *scalar for a [rows, cols] view with row
+ *                   stride ld; a no-op when *scalar == 1 (device scalar, read
+ *                   on the device).
+ */
+int rh_gelu_fwd(int dtype, int64_t n, const void* x, void* y, void* stream);
+int rh_gelu_bwd(int dtype, int64_t n, const void* x, const void* dy, void* dx, void* stream);
+int rh_add(int dtype, int64_t n, const void* a, const void* b, void* out, void* stream);
+int rh_scale_by(int dtype, int64_t rows, int64_t cols, int64_t ld, void* x, const float* scalar,
+                void* stream);
+
+/* ---- optimizer steps ------------------------------------------------------------
+ * rh_sgd_step   : p <- p - lr*(g + weight_decay*p)   (plain SGD; the cfg1 step)
+ * rh_adamw_step : torch.optim.AdamW update with the reference's constants
+ *                 (resihp/reference.py:20-38): decoupled decay
+ *                 p *= 1 - lr*wd; m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*g^2;
+ *                 p -= (lr/bias_c1) * m / (sqrt(v)/sqrt(bias_c2) + eps).
+ *                 exp_avg / exp_avg_sq have the parameter's dtype.
+ */
+int rh_sgd_step(int dtype, int64_t n, void* param, const void* grad, float lr,
+                float weight_decay, void* stream);
+int rh_adamw_step(int dtype, int64_t n, void* param, const void* grad, void* exp_avg,
+                  void* exp_avg_sq, float lr, float beta1, float beta2, float eps,
+                  float weight_decay, float bias_c1, float bias_c2, void* stream);
+
+/* ---- next-token cross-entropy ---------------------------------------------------
+ * Replaces next_token_loss = F.cross_entropy(logits[:, :-1].reshape(-1, V),
+ * tokens[:, 1:].reshape(-1)) (resihp/reference.py:41-50; called at
+ * resihp/parallel/pp.py:379-383) without materialising the shifted copy.
+ * logits [batch, seq, vocab] with row stride ld (>= vocab); tokens int64
+ * [batch, seq].  Rows s < seq-1 are scored against tokens[b, s+1]; the mean is
+ * over N = batch*(seq-1) rows.  Outputs: row_lse [batch*seq] fp32 (log-sum-exp
+ * of each row), loss [1] fp32 (the mean).  When dlogits != NULL the gradient
+ * of the mean is written too:  (softmax - onehot)/N on scored rows, 0 on the
+ * last position of every sequence and in pad columns [vocab, ld_d).
+ * Token ids outside [0, vocab) are rejected on the device: the row's loss
+ * becomes NaN.
+ * rh_xent_bwd recomputes the same gradient scaled by *grad_loss.
+ */
+int rh_xent_workspace_bytes(int64_t batch, int64_t seq, int64_t* bytes);
+int rh_xent_fwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void* logits,
+                int64_t ld, const int64_t* tokens, float* row_lse, float* loss, void* dlogits,
+                int64_t ld_d, void* workspace, int64_t workspace_bytes, void* stream);
+int rh_xent_bwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void* logits,
+                int64_t ld, const int64_t* tokens, const float* row_lse, const float* grad_loss,
+                void* dlogits, int64_t ld_d, void* stream);
+
+/* ---- embeddings ------------------------------------------------------------------
+ * Forward: out[b,s,:] = tok[ids[b,s] - vocab_start, :] (zero row when the id is
+ * outside [vocab_start, vocab_start + vocab_rows): the vocab-parallel lookup
+ * of resihp/parallel/tp.py:222-228) + pos[s, :] (pos may be NULL;
+ * resihp/model.py:128-129, resihp/parallel/tp.py:256-257).
+ * Backward: dtok[id - vocab_start] (+)= sum of dout rows with that id, in
+ * ascending token order (deterministic; duplicate ids are summed), and
+ * dpos[s] (+)= sum over batch of dout[b, s].  Either gradient may be NULL.
+ */
+int rh_embedding_fwd(int dtype, int64_t batch, int64_t seq, int64_t dim, const int64_t* tokens,
+                     const void* tok, int64_t vocab_start, int64_t vocab_rows, const void* pos,
+                     void* out, void* stream);
+int rh_embedding_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t* bytes);
+int rh_embedding_bwd(int dtype, int64_t batch, int64_t seq, int64_t dim, const int64_t* tokens,
+                     const void* dout, int64_t vocab_start, int64_t vocab_rows, void* dtok,
+                     void* dpos, int accumulate, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/* ---- TP re-slice (bit-exact byte movement) -----------------------------------------
+ * rh_reshard_pack   : dst = torch.cat(src[0..n_src), dim=shard_dim)
+ *                     (reconstruct_full, resihp/parallel/reshard.py:84-104; with
+ *                     consecutive old shards this is the TP4->TP2 new shard
+ *                     cat(old[2r], old[2r+1]) without building the full tensor).
+ *                     dim 0: src i is [extent[i], cols], dst [sum extent, cols];
+ *                     dim 1: src i is [rows, extent[i]], dst [rows, sum extent].
+ * rh_reshard_unpack : dst[i] = torch.chunk(src, ., dim=shard_dim)[i].contiguous()
+ *                     for the given extents (local_slice / shard_logical_state,
+ *                     reshard.py:107-123).
+ * Sources and destinations are contiguous; elem_bytes is the element size.
+ * A NULL destination in rh_reshard_unpack skips that extent (so one call can
+ * cut out a single new shard).
+ *
+ * rh_copy2d_batch   : n independent strided byte copies
+ *                     dst[r*dst_ld + c] = src[r*src_ld + c], r < rows,
+ *                     c < row_bytes -- the general re-slice for shard ranges
+ *                     that straddle old shards (old_size % new_size != 0).
+ */
+typedef struct rh_copy2d {
+  const void* src;
+  void* dst;
+  int64_t src_ld_bytes;
+  int64_t dst_ld_bytes;
+  int64_t rows;
+  int64_t row_bytes;
+} rh_copy2d;
+
+int rh_copy2d_batch(const rh_copy2d* segs, int n, void* stream);
+int rh_reshard_pack(const void* const* src, const int64_t* extent, int n_src, int64_t rows,
+                    int64_t cols, int shard_dim, int64_t elem_bytes, void* dst, void* stream);
+int rh_reshard_unpack(const void* src, int64_t rows, int64_t cols, int shard_dim,
+                      int64_t elem_bytes, int n_dst, void* const* dst, const int64_t* extent,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RESIHP_HIP_H */

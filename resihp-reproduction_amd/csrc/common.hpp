@@ -1,0 +1,123 @@
+// Shared device/host helpers for the resihp HIP library (gfx950 / CDNA4).
+//
+// Storage types: fp32 (`float`) and bf16 (raw `uint16_t`, round-to-nearest-even
+// on store, identical to torch's float->bfloat16 conversion). Every kernel
+// accumulates in fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include <type_traits>
+
+#include "../../include/resihp_hip.h"
+
+typedef uint16_t bf16_t;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __host__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  uint32_t u = ((uint32_t)v) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__device__ __host__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T> struct Storage;
+template <> struct Storage<float> {
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static float to_f32(float v) { return v; }
+  __device__ __forceinline__ static float from_f32(float v) { return v; }
+};
+template <> struct Storage<bf16_t> {
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+  __device__ __forceinline__ static float to_f32(bf16_t v) { return bf16_to_f32(v); }
+  __device__ __forceinline__ static bf16_t from_f32(float v) { return f32_to_bf16(v); }
+};
+
+template <typename T> __device__ __forceinline__ float ld_f32(const T* p) { return Storage<T>::load(p); }
+template <typename T> __device__ __forceinline__ void st_f32(T* p, float v) { Storage<T>::store(p, v); }
+
+// ---------------------------------------------------------------------------
+// GELU (exact, erf form) and its derivative.  HIP's own erff/expf are used.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gelu_f(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+__device__ __forceinline__ float gelu_grad_f(float x) {
+  const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
+  const float pdf = expf(-0.5f * x * x) * 0.39894228040143267794f;
+  return cdf + x * pdf;
+}
+
+// ---------------------------------------------------------------------------
+// wavefront (64-lane) reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide sum for a 1-D block of `nthreads` (multiple of 64, <= 1024).
+// `scratch` must hold nthreads/64 floats.  Result is broadcast to all threads.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int i = 0; i < nw; ++i) r += scratch[i];
+  return r;
+}
+__device__ __forceinline__ float block_max(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = -INFINITY;
+  for (int i = 0; i < nw; ++i) r = fmaxf(r, scratch[i]);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing (defined in abi.cpp)
+// ---------------------------------------------------------------------------
+int rh_set_error(int code, const char* fmt, ...);
+int rh_check_launch(const char* what);
+
+#define RH_REQUIRE(cond, ...)                                   \
+  do {                                                          \
+    if (!(cond)) return rh_set_error(RH_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+static inline int64_t rh_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+static inline bool rh_aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
+}

@@ -1,0 +1,336 @@
+// LayerNorm over the last dimension (eps, biased variance) and its backward,
+// as bandwidth-bound kernels: one wavefront per row, the row held in registers,
+// shuffle reductions, fp32 statistics.
+//
+// Forward reads x once and writes y once (plus 8 bytes of stats per row).
+// Backward reads dy, x (and the optional residual gradient) once and writes dx
+// once; the gamma/beta column sums are accumulated per lane across the rows a
+// wave visits, combined across the block's waves in LDS, written as one fp32
+// partial row per block, and summed over blocks in block order by a second
+// kernel (deterministic, no atomics).
+#include "common.hpp"
+
+namespace {
+
+// Row element e of lane l:  V == 8 : column 8*(l + 64*(e/8)) + e%8   (16-byte chunks)
+//                           V == 1 : column l + 64*e                  (scalar)
+template <int V>
+__device__ __forceinline__ int col_of(int lane, int e) {
+  return V == 8 ? 8 * (lane + 64 * (e / 8)) + (e % 8) : lane + 64 * e;
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void load_v(const T* p, float* out) {
+  if constexpr (V == 1) {
+    out[0] = ld_f32(p);
+  } else if constexpr (std::is_same<T, bf16_t>::value) {
+    const u16x8_t u = *reinterpret_cast<const u16x8_t*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = bf16_to_f32(u[j]);
+  } else {
+    const floatx4_t a = *reinterpret_cast<const floatx4_t*>(p);
+    const floatx4_t b = *reinterpret_cast<const floatx4_t*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { out[j] = a[j]; out[4 + j] = b[j]; }
+  }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void store_v(T* p, const float* in) {
+  if constexpr (V == 1) {
+    st_f32(p, in[0]);
+  } else if constexpr (std::is_same<T, bf16_t>::value) {
+    u16x8_t u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u[j] = f32_to_bf16(in[j]);
+    *reinterpret_cast<u16x8_t*>(p) = u;
+  } else {
+    floatx4_t a, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { a[j] = in[j]; b[j] = in[4 + j]; }
+    *reinterpret_cast<floatx4_t*>(p) = a;
+    *reinterpret_cast<floatx4_t*>(p + 4) = b;
+  }
+}
+
+// E = register elements per lane (multiple of V).  Elements with column >= dim
+// are skipped (loads give 0).
+template <typename T, int V, int E>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(int64_t rows, int dim, const T* __restrict__ x,
+                                                      const T* __restrict__ gamma, const T* __restrict__ beta,
+                                                      float eps, T* __restrict__ y, float* __restrict__ mean,
+                                                      float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * dim;
+  float v[E];
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; e += V) {
+    const int c = col_of<V>(lane, e);
+    if (c < dim) load_v<T, V>(xr + c, v + e);
+    else
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[e + j] = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) s += v[e + j];
+  }
+  const float mu = wave_sum(s) / (float)dim;
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; e += V) {
+    const int c = col_of<V>(lane, e);
+    if (c < dim)
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float d = v[e + j] - mu;
+        q += d * d;
+      }
+  }
+  const float var = wave_sum(q) / (float)dim;
+  const float rs = 1.0f / sqrtf(var + eps);
+  T* yr = y + row * dim;
+#pragma unroll
+  for (int e = 0; e < E; e += V) {
+    const int c = col_of<V>(lane, e);
+    if (c >= dim) continue;
+    float gv[V], bv[V], o[V];
+    load_v<T, V>(gamma + c, gv);
+    load_v<T, V>(beta + c, bv);
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] = (v[e + j] - mu) * rs * gv[j] + bv[j];
+    store_v<T, V>(yr + c, o);
+  }
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+template <typename T, int V, int E>
+__global__ __launch_bounds__(256) void ln_bwd_kernel(int64_t rows, int dim, const T* __restrict__ dy,
+                                                      const T* __restrict__ x, const float* __restrict__ mean,
+                                                      const float* __restrict__ rstd, const T* __restrict__ gamma,
+                                                      const T* __restrict__ dres, T* __restrict__ dx,
+                                                      float* __restrict__ part_g, float* __restrict__ part_b) {
+  __shared__ float red[2][4][64 * 8];  // per-wave column partials for one chunk row (reused per e)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float pg[E], pb[E], gmm[E];
+#pragma unroll
+  for (int e = 0; e < E; e += V) {
+    const int c = col_of<V>(lane, e);
+    if (c < dim) load_v<T, V>(gamma + c, gmm + e);
+    else
+#pragma unroll
+      for (int j = 0; j < V; ++j) gmm[e + j] = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) { pg[e + j] = 0.f; pb[e + j] = 0.f; }
+  }
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += (int64_t)gridDim.x * 4) {
+    const T* dyr = dy + row * dim;
+    const T* xr = x + row * dim;
+    const float mu = mean[row], rs = rstd[row];
+    float xh[E], g[E];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; e += V) {
+      const int c = col_of<V>(lane, e);
+      float dv[V], xv[V];
+      if (c < dim) {
+        load_v<T, V>(dyr + c, dv);
+        load_v<T, V>(xr + c, xv);
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) { dv[j] = 0.f; xv[j] = mu; }
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float h = (xv[j] - mu) * rs;
+        xh[e + j] = h;
+        g[e + j] = dv[j] * gmm[e + j];
+        s1 += g[e + j];
+        s2 += g[e + j] * h;
+        pg[e + j] += dv[j] * h;
+        pb[e + j] += dv[j];
+      }
+    }
+    const float m1 = wave_sum(s1) / (float)dim;
+    const float m2 = wave_sum(s2) / (float)dim;
+    T* dxr = dx + row * dim;
+    const T* drr = dres ? dres + row * dim : nullptr;
+#pragma unroll
+    for (int e = 0; e < E; e += V) {
+      const int c = col_of<V>(lane, e);
+      if (c >= dim) continue;
+      float o[V], rv[V];
+      if (drr) load_v<T, V>(drr + c, rv);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        o[j] = rs * (g[e + j] - m1 - xh[e + j] * m2);
+        if (drr) o[j] += rv[j];
+      }
+      store_v<T, V>(dxr + c, o);
+    }
+  }
+  // combine the 4 waves' column partials, one V-chunk of columns at a time
+#pragma unroll
+  for (int e = 0; e < E; e += V) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      red[0][wave][lane * V + j] = pg[e + j];
+      red[1][wave][lane * V + j] = pb[e + j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * V; i += 256) {
+      const int ln = i / V, j = i % V;
+      const int col = V == 8 ? 8 * (ln + 64 * (e / 8)) + j : ln + 64 * e;
+      if (col < dim) {
+        const float sg = red[0][0][i] + red[0][1][i] + red[0][2][i] + red[0][3][i];
+        const float sb = red[1][0][i] + red[1][1][i] + red[1][2][i] + red[1][3][i];
+        part_g[(int64_t)blockIdx.x * dim + col] = sg;
+        part_b[(int64_t)blockIdx.x * dim + col] = sb;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ln_colsum_kernel(int nblocks, int dim, const float* __restrict__ part_g,
+                                                         const float* __restrict__ part_b, T* dgamma, T* dbeta,
+                                                         int accumulate) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= dim) return;
+  float sg = 0.f, sb = 0.f;
+  for (int b = 0; b < nblocks; ++b) {
+    sg += part_g[(int64_t)b * dim + col];
+    sb += part_b[(int64_t)b * dim + col];
+  }
+  if (dgamma) st_f32(dgamma + col, accumulate ? ld_f32(dgamma + col) + sg : sg);
+  if (dbeta) st_f32(dbeta + col, accumulate ? ld_f32(dbeta + col) + sb : sb);
+}
+
+int ln_blocks(int64_t rows) {
+  int64_t nb = rh_cdiv(rows, 32);
+  if (nb > 512) nb = 512;
+  if (nb < 1) nb = 1;
+  return (int)nb;
+}
+
+// Pick (V, E) for a dimension: vectorised when dim % 8 == 0 and aligned.
+template <typename T, template <typename, int, int> class Launcher, typename... Args>
+int dispatch_ln(int dim, bool vec, Args... args) {
+  if (vec) {
+    const int chunks = (dim + 511) / 512;  // 16-byte chunks per lane (8 elements each)
+    if (chunks <= 1) return Launcher<T, 8, 8>::run(args...);
+    if (chunks <= 2) return Launcher<T, 8, 16>::run(args...);
+    if (chunks <= 4) return Launcher<T, 8, 32>::run(args...);
+    if (chunks <= 8) return Launcher<T, 8, 64>::run(args...);
+    return Launcher<T, 8, 128>::run(args...);
+  }
+  const int per = (dim + 63) / 64;
+  if (per <= 1) return Launcher<T, 1, 1>::run(args...);
+  if (per <= 2) return Launcher<T, 1, 2>::run(args...);
+  if (per <= 4) return Launcher<T, 1, 4>::run(args...);
+  if (per <= 8) return Launcher<T, 1, 8>::run(args...);
+  if (per <= 16) return Launcher<T, 1, 16>::run(args...);
+  if (per <= 32) return Launcher<T, 1, 32>::run(args...);
+  if (per <= 64) return Launcher<T, 1, 64>::run(args...);
+  return Launcher<T, 1, 128>::run(args...);
+}
+
+template <typename T, int V, int E>
+struct FwdLauncher {
+  static int run(int64_t rows, int dim, const void* x, const void* g, const void* b, float eps, void* y, float* mean,
+                 float* rstd, hipStream_t st) {
+    hipLaunchKernelGGL((ln_fwd_kernel<T, V, E>), dim3((unsigned)rh_cdiv(rows, 4)), dim3(256), 0, st, rows, dim,
+                       (const T*)x, (const T*)g, (const T*)b, eps, (T*)y, mean, rstd);
+    return rh_check_launch("rh_layernorm_fwd");
+  }
+};
+
+template <typename T, int V, int E>
+struct BwdLauncher {
+  static int run(int64_t rows, int dim, const void* dy, const void* x, const float* mean, const float* rstd,
+                 const void* gamma, const void* dres, void* dx, float* pg, float* pb, int nb, hipStream_t st) {
+    hipLaunchKernelGGL((ln_bwd_kernel<T, V, E>), dim3((unsigned)nb), dim3(256), 0, st, rows, dim, (const T*)dy,
+                       (const T*)x, mean, rstd, (const T*)gamma, (const T*)dres, (T*)dx, pg, pb);
+    return rh_check_launch("rh_layernorm_bwd");
+  }
+};
+
+int check_ln(int dtype, int64_t rows, int64_t dim) {
+  RH_REQUIRE(dtype == RH_DTYPE_F32 || dtype == RH_DTYPE_BF16, "rh_layernorm: unknown dtype %d", dtype);
+  RH_REQUIRE(rows >= 0, "rh_layernorm: negative rows");
+  RH_REQUIRE(dim >= 1 && dim <= 8192, "rh_layernorm: dim %lld outside [1, 8192]", (long long)dim);
+  return RH_OK;
+}
+
+}  // namespace
+
+extern "C" int rh_layernorm_fwd(int dtype, int64_t rows, int64_t dim, const void* x, const void* gamma,
+                                const void* beta, float eps, void* y, float* mean, float* rstd, void* stream) {
+  int rc = check_ln(dtype, rows, dim);
+  if (rc) return rc;
+  if (rows == 0) return RH_OK;
+  RH_REQUIRE(x && gamma && beta && y && mean && rstd, "rh_layernorm_fwd: null pointer");
+  const bool vec = dim % 8 == 0 && rh_aligned(x, 16) && rh_aligned(y, 16) && rh_aligned(gamma, 16) &&
+                   rh_aligned(beta, 16);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == RH_DTYPE_BF16)
+    return dispatch_ln<bf16_t, FwdLauncher>((int)dim, vec, rows, (int)dim, x, gamma, beta, eps, y, mean, rstd, st);
+  return dispatch_ln<float, FwdLauncher>((int)dim, vec, rows, (int)dim, x, gamma, beta, eps, y, mean, rstd, st);
+}
+
+extern "C" int rh_layernorm_bwd_workspace_bytes(int64_t rows, int64_t dim, int64_t* bytes) {
+  RH_REQUIRE(bytes && rows >= 0 && dim >= 0, "rh_layernorm_bwd_workspace_bytes: bad arguments");
+  *bytes = 2 * (int64_t)ln_blocks(rows) * dim * (int64_t)sizeof(float);
+  return RH_OK;
+}
+
+extern "C" int rh_layernorm_bwd(int dtype, int64_t rows, int64_t dim, const void* dy, const void* x,
+                                const float* mean, const float* rstd, const void* gamma, const void* dresidual,
+                                void* dx, void* dgamma, void* dbeta, int accumulate, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  int rc = check_ln(dtype, rows, dim);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = ln_blocks(rows);
+  if (rows == 0) {
+    if (!accumulate && (dgamma || dbeta)) {
+      // empty batch: the column sums are zero
+      const int64_t eb = dtype == RH_DTYPE_BF16 ? 2 : 4;
+      if (dgamma && hipMemsetAsync(dgamma, 0, dim * eb, st) != hipSuccess)
+        return rh_set_error(RH_ERR_HIP, "rh_layernorm_bwd: memset failed");
+      if (dbeta && hipMemsetAsync(dbeta, 0, dim * eb, st) != hipSuccess)
+        return rh_set_error(RH_ERR_HIP, "rh_layernorm_bwd: memset failed");
+    }
+    return RH_OK;
+  }
+  RH_REQUIRE(dy && x && mean && rstd && gamma && dx, "rh_layernorm_bwd: null pointer");
+  RH_REQUIRE(workspace && workspace_bytes >= 2 * (int64_t)nb * dim * (int64_t)sizeof(float),
+             "rh_layernorm_bwd: workspace of %lld bytes is too small", (long long)workspace_bytes);
+  float* pg = static_cast<float*>(workspace);
+  float* pb = pg + (int64_t)nb * dim;
+  const bool vec = dim % 8 == 0 && rh_aligned(dy, 16) && rh_aligned(x, 16) && rh_aligned(dx, 16) &&
+                   rh_aligned(gamma, 16) && (dresidual == nullptr || rh_aligned(dresidual, 16));
+  if (dtype == RH_DTYPE_BF16)
+    rc = dispatch_ln<bf16_t, BwdLauncher>((int)dim, vec, rows, (int)dim, dy, x, mean, rstd, gamma, dresidual, dx, pg,
+                                          pb, nb, st);
+  else
+    rc = dispatch_ln<float, BwdLauncher>((int)dim, vec, rows, (int)dim, dy, x, mean, rstd, gamma, dresidual, dx, pg,
+                                         pb, nb, st);
+  if (rc) return rc;
+  if (dgamma || dbeta) {
+    const unsigned blocks = (unsigned)rh_cdiv(dim, 256);
+    if (dtype == RH_DTYPE_BF16)
+      hipLaunchKernelGGL(ln_colsum_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, nb, (int)dim, pg, pb,
+                         (bf16_t*)dgamma, (bf16_t*)dbeta, accumulate);
+    else
+      hipLaunchKernelGGL(ln_colsum_kernel<float>, dim3(blocks), dim3(256), 0, st, nb, (int)dim, pg, pb,
+                         (float*)dgamma, (float*)dbeta, accumulate);
+    return rh_check_launch("rh_layernorm_bwd colsum");
+  }
+  return RH_OK;
+}

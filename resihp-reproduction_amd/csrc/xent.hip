@@ -1,0 +1,230 @@
+// Next-token softmax cross-entropy over [batch, seq, vocab] logits, forward and
+// backward, without materialising logits[:, :-1] or a one-hot matrix.
+//
+// One 256-thread block per logits row.  Pass 1 streams the row once with
+// 16-byte loads and keeps a per-thread online (max, sum-exp) pair, merged
+// across the block.  When the gradient is wanted in the same call, pass 2
+// re-reads the row (still resident in L2) and writes
+//   dlogits = (exp(x - lse) - [j == target]) / N
+// so the fused forward+backward moves 2 bytes in and 2 bytes out per bf16
+// logit.  Row losses are reduced to the mean by a single block in a fixed
+// order (deterministic).
+#include "common.hpp"
+
+namespace {
+
+constexpr int kT = 256;
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* v) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    const u16x8_t u = *reinterpret_cast<const u16x8_t*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = bf16_to_f32(u[j]);
+  } else {
+    const floatx4_t a = *reinterpret_cast<const floatx4_t*>(p);
+    const floatx4_t b = *reinterpret_cast<const floatx4_t*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* v) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    u16x8_t u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u[j] = f32_to_bf16(v[j]);
+    *reinterpret_cast<u16x8_t*>(p) = u;
+  } else {
+    floatx4_t a, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { a[j] = v[j]; b[j] = v[4 + j]; }
+    *reinterpret_cast<floatx4_t*>(p) = a;
+    *reinterpret_cast<floatx4_t*>(p + 4) = b;
+  }
+}
+
+// Row log-sum-exp.  VEC: row start 16-byte aligned -> 8-wide loads.
+template <typename T, bool VEC>
+__device__ float row_lse(const T* x, int64_t V, float* scratch) {
+  float m = -INFINITY, s = 0.f;
+  if (VEC) {
+    const int64_t full = V / 8 * 8;
+    for (int64_t j = (int64_t)threadIdx.x * 8; j < full; j += kT * 8) {
+      float v[8];
+      load8<T>(x + j, v);
+      float cm = v[0];
+#pragma unroll
+      for (int t = 1; t < 8; ++t) cm = fmaxf(cm, v[t]);
+      const float mn = fmaxf(m, cm);
+      float acc = s * expf(m - mn);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc += expf(v[t] - mn);
+      s = acc;
+      m = mn;
+    }
+    for (int64_t j = full + threadIdx.x; j < V; j += kT) {
+      const float v = ld_f32(x + j);
+      const float mn = fmaxf(m, v);
+      s = s * expf(m - mn) + expf(v - mn);
+      m = mn;
+    }
+  } else {
+    for (int64_t j = threadIdx.x; j < V; j += kT) {
+      const float v = ld_f32(x + j);
+      const float mn = fmaxf(m, v);
+      s = s * expf(m - mn) + expf(v - mn);
+      m = mn;
+    }
+  }
+  const float M = block_max(m, scratch);
+  const float part = (m == -INFINITY) ? 0.f : s * expf(m - M);
+  const float tot = block_sum(part, scratch + 8);
+  return M + logf(tot);
+}
+
+// dlogits row: (exp(x - lse) - [j == tgt]) * scale over [0, V), zero on [V, ld_d).
+template <typename T, bool VEC>
+__device__ void row_grad(const T* x, T* d, int64_t V, int64_t ld_d, float lse, int64_t tgt, float scale) {
+  if (VEC) {
+    const int64_t full = V / 8 * 8;
+    for (int64_t j = (int64_t)threadIdx.x * 8; j < full; j += kT * 8) {
+      float v[8];
+      load8<T>(x + j, v);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = (expf(v[t] - lse) - ((j + t) == tgt ? 1.f : 0.f)) * scale;
+      store8<T>(d + j, v);
+    }
+    for (int64_t j = full + threadIdx.x; j < V; j += kT)
+      st_f32(d + j, (expf(ld_f32(x + j) - lse) - (j == tgt ? 1.f : 0.f)) * scale);
+  } else {
+    for (int64_t j = threadIdx.x; j < V; j += kT)
+      st_f32(d + j, (expf(ld_f32(x + j) - lse) - (j == tgt ? 1.f : 0.f)) * scale);
+  }
+  for (int64_t j = V + threadIdx.x; j < ld_d; j += kT) st_f32(d + j, 0.f);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kT) void xent_fwd_kernel(int S, int64_t V, const T* __restrict__ logits, int64_t ld,
+                                                       const int64_t* __restrict__ tokens, float* __restrict__ lse_out,
+                                                       float* __restrict__ loss_rows, T* dl, int64_t ld_d,
+                                                       float inv_n) {
+  __shared__ float scratch[16];
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  const T* x = logits + row * ld;
+  if (s == S - 1) {
+    if (threadIdx.x == 0) {
+      loss_rows[row] = 0.f;
+      lse_out[row] = 0.f;
+    }
+    if (dl)
+      for (int64_t j = threadIdx.x; j < ld_d; j += kT) st_f32(dl + row * ld_d + j, 0.f);
+    return;
+  }
+  const float lse = row_lse<T, VEC>(x, V, scratch);
+  const int64_t tgt = tokens[row + 1];
+  if (threadIdx.x == 0) {
+    const float xt = (tgt >= 0 && tgt < V) ? ld_f32(x + tgt) : NAN;
+    loss_rows[row] = lse - xt;
+    lse_out[row] = lse;
+  }
+  if (dl) row_grad<T, VEC>(x, dl + row * ld_d, V, ld_d, lse, tgt, inv_n);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kT) void xent_bwd_kernel(int S, int64_t V, const T* __restrict__ logits, int64_t ld,
+                                                       const int64_t* __restrict__ tokens,
+                                                       const float* __restrict__ lse_in, const float* grad_loss,
+                                                       T* dl, int64_t ld_d, float inv_n) {
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  if (s == S - 1) {
+    for (int64_t j = threadIdx.x; j < ld_d; j += kT) st_f32(dl + row * ld_d + j, 0.f);
+    return;
+  }
+  const float scale = inv_n * (grad_loss ? *grad_loss : 1.f);
+  row_grad<T, VEC>(logits + row * ld, dl + row * ld_d, V, ld_d, lse_in[row], tokens[row + 1], scale);
+}
+
+__global__ __launch_bounds__(1024) void mean_kernel(int64_t n, const float* __restrict__ rows, float inv_n,
+                                                    float* __restrict__ out) {
+  __shared__ float scratch[16];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += rows[i];
+  const float tot = block_sum(s, scratch);
+  if (threadIdx.x == 0) out[0] = tot * inv_n;
+}
+
+int check_xent(int dtype, int64_t B, int64_t S, int64_t V, int64_t ld) {
+  RH_REQUIRE(dtype == RH_DTYPE_F32 || dtype == RH_DTYPE_BF16, "rh_xent: unknown dtype %d", dtype);
+  RH_REQUIRE(B >= 1 && S >= 2, "rh_xent: need batch >= 1 and seq >= 2 (got %lld, %lld)", (long long)B, (long long)S);
+  RH_REQUIRE(V >= 1 && ld >= V, "rh_xent: vocab %lld / ld %lld invalid", (long long)V, (long long)ld);
+  RH_REQUIRE(B * S <= INT32_MAX, "rh_xent: too many rows");
+  return RH_OK;
+}
+
+}  // namespace
+
+extern "C" int rh_xent_workspace_bytes(int64_t batch, int64_t seq, int64_t* bytes) {
+  RH_REQUIRE(bytes && batch >= 0 && seq >= 0, "rh_xent_workspace_bytes: bad arguments");
+  *bytes = batch * seq * (int64_t)sizeof(float);
+  return RH_OK;
+}
+
+extern "C" int rh_xent_fwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void* logits, int64_t ld,
+                           const int64_t* tokens, float* row_lse, float* loss, void* dlogits, int64_t ld_d,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_xent(dtype, batch, seq, vocab, ld);
+  if (rc) return rc;
+  RH_REQUIRE(logits && tokens && row_lse && loss, "rh_xent_fwd: null pointer");
+  if (dlogits) RH_REQUIRE(ld_d >= vocab, "rh_xent_fwd: ld_d %lld < vocab", (long long)ld_d);
+  RH_REQUIRE(workspace && workspace_bytes >= batch * seq * (int64_t)sizeof(float),
+             "rh_xent_fwd: workspace of %lld bytes is too small", (long long)workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* rows = static_cast<float*>(workspace);
+  const int64_t nrows = batch * seq;
+  const float inv_n = 1.0f / (float)(batch * (seq - 1));
+  const bool vec = rh_aligned(logits, 16) && ld % 8 == 0 && (!dlogits || (rh_aligned(dlogits, 16) && ld_d % 8 == 0));
+  if (dtype == RH_DTYPE_BF16) {
+    if (vec) hipLaunchKernelGGL((xent_fwd_kernel<bf16_t, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                                (const bf16_t*)logits, ld, tokens, row_lse, rows, (bf16_t*)dlogits, ld_d, inv_n);
+    else hipLaunchKernelGGL((xent_fwd_kernel<bf16_t, false>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                            (const bf16_t*)logits, ld, tokens, row_lse, rows, (bf16_t*)dlogits, ld_d, inv_n);
+  } else {
+    if (vec) hipLaunchKernelGGL((xent_fwd_kernel<float, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                                (const float*)logits, ld, tokens, row_lse, rows, (float*)dlogits, ld_d, inv_n);
+    else hipLaunchKernelGGL((xent_fwd_kernel<float, false>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                            (const float*)logits, ld, tokens, row_lse, rows, (float*)dlogits, ld_d, inv_n);
+  }
+  rc = rh_check_launch("rh_xent_fwd");
+  if (rc) return rc;
+  hipLaunchKernelGGL(mean_kernel, dim3(1), dim3(1024), 0, st, nrows, rows, inv_n, loss);
+  return rh_check_launch("rh_xent_fwd mean");
+}
+
+extern "C" int rh_xent_bwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void* logits, int64_t ld,
+                           const int64_t* tokens, const float* row_lse, const float* grad_loss, void* dlogits,
+                           int64_t ld_d, void* stream) {
+  int rc = check_xent(dtype, batch, seq, vocab, ld);
+  if (rc) return rc;
+  RH_REQUIRE(logits && tokens && row_lse && dlogits, "rh_xent_bwd: null pointer");
+  RH_REQUIRE(ld_d >= vocab, "rh_xent_bwd: ld_d %lld < vocab", (long long)ld_d);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nrows = batch * seq;
+  const float inv_n = 1.0f / (float)(batch * (seq - 1));
+  const bool vec = rh_aligned(logits, 16) && ld % 8 == 0 && rh_aligned(dlogits, 16) && ld_d % 8 == 0;
+  if (dtype == RH_DTYPE_BF16) {
+    if (vec) hipLaunchKernelGGL((xent_bwd_kernel<bf16_t, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                                (const bf16_t*)logits, ld, tokens, row_lse, grad_loss, (bf16_t*)dlogits, ld_d, inv_n);
+    else hipLaunchKernelGGL((xent_bwd_kernel<bf16_t, false>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                            (const bf16_t*)logits, ld, tokens, row_lse, grad_loss, (bf16_t*)dlogits, ld_d, inv_n);
+  } else {
+    if (vec) hipLaunchKernelGGL((xent_bwd_kernel<float, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                                (const float*)logits, ld, tokens, row_lse, grad_loss, (float*)dlogits, ld_d, inv_n);
+    else hipLaunchKernelGGL((xent_bwd_kernel<float, false>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+                            (const float*)logits, ld, tokens, row_lse, grad_loss, (float*)dlogits, ld_d, inv_n);
+  }
+  return rh_check_launch("rh_xent_bwd");
+}
