@@ -1,0 +1,417 @@
+"""Throughput of the decoder-LM forward+backward hot path on one MI355X.
+
+Default workload: one TP=4 rank's shard of a GPT-1.3B-shape block (d_model 2048,
+4 of 16 heads local with head_dim 128, column-parallel QKV 2048->1536 and FC1
+2048->2048, row-parallel out-proj 512->2048 and FC2 2048->2048 emitting partial
+sums), seq 2048, micro-batch 4, bf16 with fp32 accumulation; input activations
+N(0,1), upstream gradients N(0, 1e-2), weights N(0, 0.02).  A step is one
+forward + backward of that shard with fresh parameter gradients.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-graph]
+
+Prints ONE JSON line.  `value` is tokens/s of the whole job (one GPU).  The
+timed region replays a HIP graph of the step (captured after the warm-up and
+checked bit-for-bit against an eager step) unless --no-graph is given.  The
+roofline object is measured in a separate eager pass with HIP events around
+each launch of the dominant kernel.  The CPU baseline is the oracle's torch-CPU
+restatement of the same step, timed on a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT / "resihp-reproduction_amd"), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "train tokens/sec/GPU (fwd+bwd) per shard; MFMA util % and HBM GB/s"
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA FLOP/s
+PEAK_HBM = 8.0e12  # bytes/s
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+class Workload:
+    name = ""
+    tokens = 0
+    flops = 0.0
+    config: dict = {}
+
+    def setup(self, dev):
+        raise NotImplementedError
+
+    def step(self):
+        raise NotImplementedError
+
+    def outputs(self):
+        """Tensors whose values identify a step's result (for the graph-vs-eager check)."""
+        raise NotImplementedError
+
+    def zero_grads(self):
+        for p in self.params():
+            p.grad = None
+
+    def release(self):
+        """Drop the last step's outputs, and with them its autograd graph."""
+        self.out = None
+        self.loss = None
+
+    def params(self):
+        return []
+
+    def cpu_sample(self, budget_s: float) -> dict:
+        raise NotImplementedError
+
+
+def _block_fwd_flops(tokens, d, dl, ff, batch, heads_local, head_dim, seq):
+    gemm = 2.0 * tokens * (d * 3 * dl + dl * d + d * ff + ff * d)
+    attn = 4.0 * batch * heads_local * head_dim * seq * (seq + 1) / 2
+    return gemm, attn
+
+
+class ShardBlock(Workload):
+    """One TP rank's shard of one decoder block (middle pipeline stage)."""
+
+    def __init__(self, name, d=2048, heads=16, tp=4, rank=2, seq=2048, batch=4, layers=1):
+        self.name, self.d, self.heads, self.tp, self.rank = name, d, heads, tp, rank
+        self.seq, self.batch, self.layers = seq, batch, layers
+        self.tokens = seq * batch
+        dl, ff = d // tp, 4 * d // tp
+        g, a = _block_fwd_flops(self.tokens, d, dl, ff, batch, heads // tp, d // heads, seq)
+        self.gemm_flops_fwd, self.attn_flops_fwd = g * layers, a * layers
+        self.flops = 3.0 * (self.gemm_flops_fwd + self.attn_flops_fwd)
+        self.config = {"workload": name, "d_model": d, "heads_total": heads, "heads_local": heads // tp,
+                       "head_dim": d // heads, "tp_size": tp, "tp_rank": rank, "seq_len": seq, "micro_batch": batch,
+                       "layers": layers, "tokens_per_step": self.tokens,
+                       "gemms": {"qkv": [self.tokens, 3 * dl, d], "out": [self.tokens, d, dl],
+                                 "fc1": [self.tokens, ff, d], "fc2": [self.tokens, d, ff]},
+                       "parallelism": f"one TP={tp} rank on 1 GPU, no collectives (row-parallel partial sums)"}
+
+    def _state(self):
+        from oracle import torch_ref  # synthetic weights only (same generator as the tests)
+        import torch
+
+        st = torch_ref.synthetic_state(self.d, self.layers, 8 * self.tp, self.seq, std=0.02, seed=0, first=False,
+                                       last=False, tp_size=self.tp, tp_rank=self.rank)
+        return {k: v.to(torch.bfloat16) for k, v in st.items()}
+
+    def setup(self, dev):
+        import torch
+
+        from resihp.config import TrainConfig
+        from resihp.parallel.tp import TensorParallelStage
+
+        cfg = TrainConfig(model_dim=self.d, num_layers=self.layers, num_heads=self.heads, batch_size=self.batch,
+                          micro_batch_size=self.batch, seed=0, tp=self.tp, pp=1, dp=1, iterations=1)
+        local = {k: v.to(dev) for k, v in self._state().items()}
+        self.stage = TensorParallelStage(cfg, vocab_size=8 * self.tp, sequence_length=self.seq,
+                                         layer_ids=range(self.layers), is_first=False, is_last=False,
+                                         local_state=local, tp_rank=self.rank, tp_size=self.tp)
+        g = torch.Generator().manual_seed(1)
+        self.x = torch.randn(self.batch, self.seq, self.d, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+        self.dy = (torch.randn(self.batch, self.seq, self.d, generator=g) * 1e-2).to(dev, torch.bfloat16)
+
+    def params(self):
+        return list(self.stage.parameters()) + [self.x]
+
+    def step(self):
+        self.out = self.stage(hidden=self.x)
+        self.out.backward(self.dy)
+
+    def outputs(self):
+        return [self.out] + [p.grad for p in self.params()]
+
+    def cpu_sample(self, budget_s):
+        import torch
+
+        from oracle import torch_ref
+
+        st = {k: v.float().requires_grad_(True) for k, v in self._state().items()}
+        g = torch.Generator().manual_seed(1)
+        mb = 1
+        x = torch.randn(mb, self.seq, self.d, generator=g).requires_grad_(True)
+        dy = torch.randn(mb, self.seq, self.d, generator=g) * 1e-2
+
+        def one():
+            out = torch_ref.shard_forward(st, num_heads=self.heads, tp_rank=self.rank, tp_size=self.tp,
+                                          vocab_size=8 * self.tp, layer_ids=range(self.layers), is_first=False,
+                                          is_last=False, hidden=x)
+            out.backward(dy)
+
+        one()  # warm-up
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            one()
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or steps >= 20:
+                break
+        return {"tokens": mb * self.seq * steps, "seconds": el,
+                "sample": f"{steps} fwd+bwd of the same shard at micro-batch {mb} (seq {self.seq}), fp32, "
+                          f"oracle torch-CPU restatement"}
+
+
+class GPT2Small(Workload):
+    """The full GPT-2-small-shape LM: 12 layers, d 768, 12 heads, FFN 3072, vocab 50257, seq 1024, batch 8."""
+
+    def __init__(self, name="gpt2_small_lm", layers=12, d=768, heads=12, vocab=50257, seq=1024, batch=8):
+        self.name, self.layers, self.d, self.heads, self.vocab = name, layers, d, heads, vocab
+        self.seq, self.batch = seq, batch
+        self.tokens = seq * batch
+        g, a = _block_fwd_flops(self.tokens, d, d, 4 * d, batch, heads, d // heads, seq)
+        self.flops = 3.0 * (layers * (g + a) + 2.0 * self.tokens * d * vocab)
+        self.config = {"workload": name, "layers": layers, "d_model": d, "heads": heads, "ffn": 4 * d,
+                       "vocab": vocab, "seq_len": seq, "batch": batch, "tokens_per_step": self.tokens,
+                       "parallelism": "single GPU, whole model"}
+
+    def setup(self, dev):
+        import torch
+
+        from resihp.config import TrainConfig
+        from resihp.model import ReferenceTransformer
+
+        cfg = TrainConfig(model_dim=self.d, num_layers=self.layers, num_heads=self.heads, batch_size=self.batch,
+                          micro_batch_size=self.batch, seed=0, tp=1, pp=1, dp=1, iterations=1)
+        torch.manual_seed(0)
+        self.model = ReferenceTransformer(cfg, vocab_size=self.vocab, sequence_length=self.seq)
+        with torch.no_grad():
+            for n, p in self.model.named_parameters():
+                if "norm" not in n:
+                    p.normal_(0.0, 0.02)
+        self.model = self.model.to(dev, torch.bfloat16)
+        g = torch.Generator().manual_seed(1)
+        self.tok = torch.randint(0, self.vocab, (self.batch, self.seq), generator=g).to(dev)
+
+    def params(self):
+        return list(self.model.parameters())
+
+    def step(self):
+        from resihp.reference import next_token_loss
+
+        self.loss = next_token_loss(self.model(self.tok), self.tok, self.vocab)
+        self.loss.backward()
+
+    def outputs(self):
+        return [self.loss] + [p.grad for p in self.params()]
+
+    def cpu_sample(self, budget_s):
+        import torch
+
+        from oracle import torch_ref
+
+        st = torch_ref.synthetic_state(self.d, self.layers, self.vocab, self.seq, std=0.02, seed=0)
+        st = {k: v.requires_grad_(True) for k, v in st.items()}
+        bsz = 1
+        tok = torch.randint(0, self.vocab, (bsz, self.seq), generator=torch.Generator().manual_seed(1))
+
+        def one():
+            logits = torch_ref.model_forward(st, tok, self.heads, range(self.layers))
+            torch_ref.next_token_loss(logits, tok, self.vocab).backward()
+
+        one()
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            one()
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or steps >= 20:
+                break
+        return {"tokens": bsz * self.seq * steps, "seconds": el,
+                "sample": f"{steps} fwd+bwd of the whole LM at batch {bsz}, fp32, oracle torch-CPU restatement"}
+
+
+class PPStage(ShardBlock):
+    """One 1F1B pipeline stage: 6 of 24 layers (d 2048, 16 heads, FFN 8192), 8 micro-batches of 2x2048."""
+
+    def __init__(self, name="pp_stage_1f1b"):
+        super().__init__(name, d=2048, heads=16, tp=1, rank=0, seq=2048, batch=2, layers=6)
+        self.micro = 8
+        self.tokens = self.micro * self.batch * self.seq
+        self.flops *= self.micro
+        self.config.update({"micro_batches": self.micro, "stage_index": 1, "num_stages": 4,
+                            "tokens_per_step": self.tokens, "parallelism": "one PP stage (1F1B order) on 1 GPU"})
+
+    def setup(self, dev):
+        import torch
+
+        super().setup(dev)
+        g = torch.Generator().manual_seed(2)
+        self.xs = [torch.randn(self.batch, self.seq, self.d, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+                   for _ in range(self.micro)]
+        self.dys = [(torch.randn(self.batch, self.seq, self.d, generator=g) * 1e-2).to(dev, torch.bfloat16)
+                    for _ in range(self.micro)]
+
+    def params(self):
+        return list(self.stage.parameters()) + self.xs
+
+    def step(self):
+        from resihp.parallel.pp import run_1f1b
+
+        run_1f1b(self.stage, stage_index=1, num_stages=4, inputs=self.xs, grads=self.dys)
+
+    def outputs(self):
+        return [p.grad for p in self.params()]
+
+
+WORKLOADS = {
+    "tp4_shard_gpt1.3b_block": lambda: ShardBlock("tp4_shard_gpt1.3b_block"),
+    "gpt2_small_lm": GPT2Small,
+    "pp_stage_1f1b": PPStage,
+    "tp2_shard_after_reshard": lambda: ShardBlock("tp2_shard_after_reshard", d=2048, heads=16, tp=2, rank=1,
+                                                  seq=2048, batch=2),
+}
+
+
+# ---------------------------------------------------------------------------
+# measurement
+# ---------------------------------------------------------------------------
+def _physical_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="tp4_shard_gpt1.3b_block", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build computes one rank's shard per GPU with no collectives "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from resihp import profiling
+
+    dev = torch.device("cuda:0")
+    wl = WORKLOADS[args.workload]()
+    _log(f"[bench] workload {wl.name}: setup")
+    wl.setup(dev)
+    for _ in range(max(1, args.warmup)):
+        wl.zero_grads()
+        wl.step()
+    torch.cuda.synchronize()
+    _log(f"[bench] warm-up done ({args.warmup} steps)")
+
+    use_graph = not args.no_graph
+    graph = None
+    if use_graph:
+        eager = [t.detach().clone() for t in wl.outputs()]
+        # A live output keeps its autograd graph -- and the AccumulateGrad nodes bound to the
+        # stream it ran on -- alive; capture must start with none of them left.
+        wl.release()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                wl.zero_grads()
+                wl.step()
+                wl.release()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        wl.zero_grads()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            wl.step()
+        for _ in range(3):  # every replay must equal the eager step
+            graph.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(wl.outputs(), eager):
+                if not torch.equal(a, b):
+                    raise RuntimeError("graph replay differs from the eager step")
+        _log("[bench] HIP graph captured; replays match the eager step bit for bit")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            wl.zero_grads()
+            wl.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    tokens_per_s = wl.tokens * args.steps / elapsed
+    tflops = wl.flops / (ms * 1e-3) / 1e12
+    _log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step, {tokens_per_s:.4g} tokens/s, {tflops:.1f} TFLOP/s")
+
+    # per-kernel roofline: eager steps with HIP events around every GEMM / attention launch
+    wl.release()
+    with profiling.record() as events:
+        for _ in range(min(args.steps, 5)):
+            wl.zero_grads()
+            wl.step()
+    torch.cuda.synchronize()
+    kernels = profiling.summary(events)
+    n_steps = min(args.steps, 5)
+    dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    dk = kernels[dominant]
+    achieved = dk["tflops"]
+    roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12,
+                "unit": "TFLOP/s", "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                "launches_per_step": dk["launches"] // n_steps, "mean_launch_us": round(dk["mean_ms"] * 1e3, 2),
+                "flops_per_launch": dk["flops_per_launch"]}
+    per_kernel = {k: {"launches_per_step": v["launches"] // n_steps, "mean_us": round(v["mean_ms"] * 1e3, 2),
+                      "tflops": round(v["tflops"], 1)} for k, v in sorted(kernels.items())}
+    _log("[bench] per-kernel: " + json.dumps(per_kernel))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cores = _physical_cores()
+        torch.set_num_threads(cores)
+        _log(f"[bench] CPU baseline on {cores} threads (budget {args.cpu_seconds}s)")
+        sample = wl.cpu_sample(args.cpu_seconds)
+        cpu = {"value": round(sample["tokens"] / sample["seconds"], 2), "unit": "tokens/s", "cores": cores,
+               "kind": "port", "sample": sample["sample"], "torch": torch.__version__}
+
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,1e-2) upstream grads, N(0,0.02) weights)",
+        "config": dict(wl.config, graph=use_graph),
+        "tflops": round(tflops, 2),
+        "mfma_frac_step": round(tflops * 1e12 / PEAK_BF16, 4),
+        "algorithmic_flops_per_step": wl.flops,
+        "roofline": roofline,
+        "kernels": per_kernel,
+        "cpu_baseline": cpu,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

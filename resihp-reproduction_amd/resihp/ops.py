@@ -22,6 +22,7 @@ import math
 import torch
 
 from . import _hip as H
+from . import profiling
 
 LN_EPS = 1e-5  # nn.LayerNorm / F.layer_norm default, resihp/model.py:89,91,115
 
@@ -119,6 +120,12 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
     desc.ldaux = ldaux
     nbytes = H.query("rh_gemm_workspace_bytes", ctypes.byref(desc))
     ws = H.workspace(nbytes, dev)
+    if profiling.active():
+        kind = "gemm_bf16_mfma" if desc.dtype == H.RH_DTYPE_BF16 else "gemm_f32_fma"
+        label = f"{kind}<{layout}, {epilogue}, {'true' if nbytes else 'false'}>"
+        with profiling.launch(label, 2.0 * M * N * K):
+            H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
+        return
     H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
 
 
@@ -236,9 +243,19 @@ def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int)
     lse = torch.empty((batch, heads, seq), dtype=torch.float32, device=qkv.device)
     es = qkv.element_size()
     base = qkv.data_ptr()
+    with profiling.launch(f"attn_fwd<{head_dim}>", attn_flops(batch, seq, heads, head_dim)):
+        _attn_fwd_call(qkv, batch, seq, heads, head_dim, dl, es, base, ctx, lse)
+    return ctx, lse
+
+
+def attn_flops(batch: int, seq: int, heads: int, head_dim: int) -> float:
+    """Causal attention forward: QK^T and PV over the lower triangle, diagonal included."""
+    return 4.0 * batch * heads * head_dim * seq * (seq + 1) / 2
+
+
+def _attn_fwd_call(qkv, batch, seq, heads, head_dim, dl, es, base, ctx, lse):
     H.call("rh_attn_fwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es, base + 2 * dl * es,
            _ld(qkv), ctx.data_ptr(), dl, lse.data_ptr(), 1.0 / math.sqrt(head_dim), 1, H.stream_of(qkv))
-    return ctx, lse
 
 
 def attn_bwd(dctx: torch.Tensor, qkv: torch.Tensor, ctx: torch.Tensor, lse: torch.Tensor, batch: int, seq: int,
@@ -251,9 +268,11 @@ def attn_bwd(dctx: torch.Tensor, qkv: torch.Tensor, ctx: torch.Tensor, lse: torc
     base, dbase = qkv.data_ptr(), dqkv.data_ptr()
     nbytes = H.query("rh_attn_bwd_workspace_bytes", batch, seq, heads)
     ws = H.workspace(nbytes, qkv.device)
-    H.call("rh_attn_bwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es, base + 2 * dl * es,
-           _ld(qkv), ctx.data_ptr(), dl, dctx.data_ptr(), _ld(dctx), lse.data_ptr(), dbase, dbase + dl * es,
-           dbase + 2 * dl * es, 3 * dl, 1.0 / math.sqrt(head_dim), 1, H.ptr(ws), nbytes, H.stream_of(qkv))
+    with profiling.launch(f"attn_bwd<{head_dim}>", 2.0 * attn_flops(batch, seq, heads, head_dim)):
+        H.call("rh_attn_bwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es,
+               base + 2 * dl * es, _ld(qkv), ctx.data_ptr(), dl, dctx.data_ptr(), _ld(dctx), lse.data_ptr(), dbase,
+               dbase + dl * es, dbase + 2 * dl * es, 3 * dl, 1.0 / math.sqrt(head_dim), 1, H.ptr(ws), nbytes,
+               H.stream_of(qkv))
     return dqkv
 
 

@@ -1,0 +1,312 @@
+"""Kernel-level parity on the GPU: every C ABI entry point against fp32 torch / the oracle.
+
+Tolerances are relative to the reference's infinity norm (max|a-b| / max|ref|):
+1e-5 for fp32 paths, bf16 paths at the storage precision (a bf16 output carries
+~4e-3 rounding), bit-exact for byte movement.
+"""
+
+import ctypes
+import math
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from conftest import rel_inf
+from oracle import torch_ref
+from resihp import _hip as H
+from resihp import ops
+from resihp.parallel import reshard
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2  # one bf16 rounding of the output plus fp32 accumulation-order noise
+F32_TOL = 1e-5
+
+
+def _rand(*shape, dtype=torch.bfloat16, scale=1.0, seed=0, dev="cuda"):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dev, dtype)
+
+
+def _gemm_ref(layout, A, B):
+    A32, B32 = A.float(), B.float()
+    if layout == H.RH_GEMM_NT:
+        return A32 @ B32.t()
+    if layout == H.RH_GEMM_NN:
+        return A32 @ B32
+    return A32.t() @ B32
+
+
+SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8, 8), (513, 257, 1000)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", [H.RH_GEMM_NT, H.RH_GEMM_NN, H.RH_GEMM_TN])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_layouts(cuda, dtype, layout, M, N, K):
+    a_shape = (K, M) if layout == H.RH_GEMM_TN else (M, K)
+    b_shape = (N, K) if layout == H.RH_GEMM_NT else (K, N)
+    A = _rand(*a_shape, dtype=dtype, seed=1)
+    B = _rand(*b_shape, dtype=dtype, seed=2)
+    D = torch.empty(M, N, dtype=dtype, device=cuda)
+    ops.gemm(layout, M, N, K, A, A.stride(0), [B], B.stride(0), [D], N)
+    err = rel_inf(D, _gemm_ref(layout, A, B))
+    assert err <= (BF16_TOL if dtype == torch.bfloat16 else F32_TOL), err
+
+
+@pytest.mark.parametrize("layout", [H.RH_GEMM_NN, H.RH_GEMM_TN])
+def test_gemm_split_k_matches_unsplit(cuda, layout):
+    """Few output tiles and a long K take the split-K path; it must agree with fp32."""
+    M, N, K = 256, 384, 8192
+    a_shape = (K, M) if layout == H.RH_GEMM_TN else (M, K)
+    A = _rand(*a_shape, seed=3)
+    B = _rand(K, N, seed=4)
+    D = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    ops.gemm(layout, M, N, K, A, A.stride(0), [B], N, [D], N)
+    assert rel_inf(D, _gemm_ref(layout, A, B)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_epilogues(cuda, dtype):
+    M, N, K = 192, 320, 256
+    A = _rand(M, K, dtype=dtype, seed=5)
+    B = _rand(N, K, dtype=dtype, seed=6, scale=0.1)
+    R = _rand(M, N, dtype=dtype, seed=7)
+    tol = BF16_TOL if dtype == torch.bfloat16 else F32_TOL
+    acc = A.float() @ B.float().t()
+    # residual: D = acc + R
+    D = torch.empty(M, N, dtype=dtype, device=cuda)
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D], N, beta=1.0, C=R, ldc=N)
+    assert rel_inf(D, acc + R.float()) <= tol
+    # alpha / in-place beta accumulate
+    D2 = R.clone()
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D2], N, alpha=0.5, beta=2.0)
+    assert rel_inf(D2, 0.5 * acc + 2 * R.float()) <= tol
+    # GELU: aux_out = pre-activation, D = gelu(pre)
+    U = torch.empty(M, N, dtype=dtype, device=cuda)
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D], N, epilogue=H.RH_EPI_GELU, aux_out=U, ldaux=N)
+    assert rel_inf(U, acc) <= tol
+    assert rel_inf(D, F.gelu(acc)) <= tol
+    # GELU_GRAD: D = acc * gelu'(aux)
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D], N, epilogue=H.RH_EPI_GELU_GRAD, aux=R, ldaux=N)
+    x = R.float().requires_grad_(True)
+    F.gelu(x).backward(acc)
+    assert rel_inf(D, x.grad) <= tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_segments_act_as_one_matrix(cuda, dtype):
+    """Three separate q/k/v weights as B segments (forward, dgrad) and as D segments (wgrad)."""
+    T, d, dl = 320, 256, 128
+    tol = BF16_TOL if dtype == torch.bfloat16 else F32_TOL
+    x = _rand(T, d, dtype=dtype, seed=8)
+    ws = [_rand(dl, d, dtype=dtype, seed=9 + i, scale=0.05) for i in range(3)]
+    W = torch.cat(ws, 0)
+    y = ops.linear_fwd(x, ws)
+    assert rel_inf(y, x.float() @ W.float().t()) <= tol
+    dy = _rand(T, 3 * dl, dtype=dtype, seed=12)
+    dx = ops.linear_dgrad(dy, ws)
+    assert rel_inf(dx, dy.float() @ W.float()) <= tol
+    params = [torch.nn.Parameter(w.clone()) for w in ws]
+    ops.linear_wgrad(dy, x, params)
+    ops.linear_wgrad(dy, x, params)  # second call accumulates into .grad
+    full = 2 * (dy.float().t() @ x.float())
+    for i, p in enumerate(params):
+        assert rel_inf(p.grad, full[i * dl:(i + 1) * dl]) <= tol
+
+
+def test_gemm_qkv_projection_at_shard_size(cuda):
+    """The one-TP-rank QKV projection of a 1.3B block: M 8192, N 1536, K 2048."""
+    x = _rand(8192, 2048, seed=13)
+    ws = [_rand(512, 2048, seed=14 + i, scale=0.02) for i in range(3)]
+    y = ops.linear_fwd(x, ws)
+    ref = x.float() @ torch.cat(ws, 0).float().t()
+    assert rel_inf(y, ref) <= 2e-2
+
+
+def _attn_ref(q, k, v, heads):
+    """fp32 reference attention on [B, S, H*Dh] rows (the reference's explicit S x S form)."""
+    B, S, W = q.shape
+    dh = W // heads
+    qh, kh, vh = (t.float().view(B, S, heads, dh).transpose(1, 2) for t in (q, k, v))
+    s = (qh @ kh.transpose(-2, -1).contiguous()) / math.sqrt(dh)
+    s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool, device=q.device), 1), float("-inf"))
+    return (torch.softmax(s, -1) @ vh).transpose(1, 2).reshape(B, S, W)
+
+
+@pytest.mark.parametrize("dtype,head_dim,seq,heads,batch", [
+    (torch.bfloat16, 128, 256, 2, 2),
+    (torch.bfloat16, 128, 200, 1, 1),
+    (torch.bfloat16, 64, 320, 3, 2),
+    (torch.bfloat16, 64, 1024, 2, 1),
+    (torch.bfloat16, 32, 96, 2, 2),
+    (torch.float32, 16, 32, 4, 4),
+    (torch.float32, 64, 130, 2, 1),
+])
+def test_attention_forward_backward(cuda, dtype, head_dim, seq, heads, batch):
+    W = heads * head_dim
+    qkv = _rand(batch * seq, 3 * W, dtype=dtype, seed=20)
+    ctx, lse = ops.attn_fwd(qkv, batch, seq, heads, head_dim)
+    q, k, v = (qkv[:, i * W:(i + 1) * W].reshape(batch, seq, W).float().requires_grad_(True) for i in range(3))
+    ref = _attn_ref(q, k, v, heads)
+    tol = 2e-2 if dtype == torch.bfloat16 else F32_TOL
+    assert rel_inf(ctx.view(batch, seq, W), ref) <= tol
+    # lse = log sum_j exp(s_ij)
+    qh = q.detach().view(batch, seq, heads, head_dim).transpose(1, 2)
+    kh = k.detach().view(batch, seq, heads, head_dim).transpose(1, 2)
+    s = (qh @ kh.transpose(-2, -1).contiguous()) / math.sqrt(head_dim)
+    s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool, device=cuda), 1), float("-inf"))
+    assert rel_inf(lse, torch.logsumexp(s, -1)) <= (1e-5 if dtype == torch.float32 else 5e-3)
+    dout = _rand(batch * seq, W, dtype=dtype, seed=21)
+    dqkv = ops.attn_bwd(dout, qkv, ctx, lse, batch, seq, heads, head_dim)
+    ref.backward(dout.float().view(batch, seq, W))
+    for i, t in enumerate((q, k, v)):
+        got = dqkv[:, i * W:(i + 1) * W].reshape(batch, seq, W)
+        assert rel_inf(got, t.grad) <= (3e-2 if dtype == torch.bfloat16 else 1e-4), ("qkv"[i], rel_inf(got, t.grad))
+
+
+@pytest.mark.parametrize("dtype,rows,dim", [(torch.float32, 64, 64), (torch.float32, 37, 100),
+                                            (torch.bfloat16, 512, 2048), (torch.bfloat16, 130, 768),
+                                            (torch.float32, 8, 5000), (torch.bfloat16, 3, 24)])
+def test_layernorm_forward_backward(cuda, dtype, rows, dim):
+    x = _rand(rows, dim, dtype=dtype, seed=30, scale=2.0) + 0.5
+    w = torch.nn.Parameter(_rand(dim, dtype=dtype, seed=31) * 0.2 + 1.0)
+    b = torch.nn.Parameter(_rand(dim, dtype=dtype, seed=32) * 0.2)
+    y, mean, rstd = ops.ln_fwd(x, w, b, 1e-5)
+    xr = x.float().requires_grad_(True)
+    wr = w.detach().float().requires_grad_(True)
+    br = b.detach().float().requires_grad_(True)
+    yr = F.layer_norm(xr, (dim,), wr, br, 1e-5)
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    assert rel_inf(y, yr) <= tol
+    dy = _rand(rows, dim, dtype=dtype, seed=33)
+    dres = _rand(rows, dim, dtype=dtype, seed=34)
+    dx = ops.ln_bwd(dy, x, mean, rstd, w, b, dres)
+    yr.backward(dy.float())
+    assert rel_inf(dx, xr.grad + dres.float()) <= (1e-4 if dtype == torch.float32 else 2e-2)
+    assert rel_inf(w.grad, wr.grad) <= (1e-4 if dtype == torch.float32 else 2e-2)
+    assert rel_inf(b.grad, br.grad) <= (1e-4 if dtype == torch.float32 else 2e-2)
+    # second backward accumulates
+    ops.ln_bwd(dy, x, mean, rstd, w, b, None)
+    assert rel_inf(w.grad, 2 * wr.grad) <= (1e-4 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype,batch,seq,vocab", [(torch.float32, 4, 32, 256), (torch.bfloat16, 2, 64, 50257),
+                                                   (torch.float32, 3, 5, 1001), (torch.bfloat16, 2, 2, 7)])
+def test_next_token_loss(cuda, dtype, batch, seq, vocab):
+    logits = _rand(batch, seq, vocab, dtype=dtype, seed=40, scale=3.0).requires_grad_(True)
+    g = torch.Generator().manual_seed(41)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g).to(cuda)
+    loss = ops.next_token_loss(logits, tokens, vocab)
+    lr = logits.detach().float().requires_grad_(True)
+    ref = torch_ref.next_token_loss(lr, tokens, vocab)
+    assert abs(float(loss) - float(ref)) <= (1e-5 if dtype == torch.float32 else 1e-3) * max(1.0, abs(float(ref)))
+    (loss * 0.5).backward()
+    (ref * 0.5).backward()
+    assert rel_inf(logits.grad, lr.grad) <= (F32_TOL if dtype == torch.float32 else BF16_TOL)
+    assert torch.all(logits.grad[:, -1] == 0)
+
+
+def test_next_token_loss_of_zero_logits_is_log_vocab(cuda):
+    logits = torch.zeros(2, 16, 1000, device=cuda)
+    tokens = torch.randint(0, 1000, (2, 16), device=cuda)
+    assert abs(float(ops.next_token_loss(logits, tokens, 1000)) - math.log(1000)) < 1e-6
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_embedding_forward_backward_deterministic(cuda, dtype):
+    vocab, dim, batch, seq = 50, 64, 4, 33
+    W = torch.nn.Parameter(_rand(vocab, dim, dtype=dtype, seed=50))
+    P = torch.nn.Parameter(_rand(seq, dim, dtype=dtype, seed=51))
+    g = torch.Generator().manual_seed(52)
+    tokens = torch.randint(0, 7, (batch, seq), generator=g).to(cuda)  # many duplicates
+    out = ops.embedding(tokens, W, P)
+    ref = F.embedding(tokens, W.detach().float()) + P.detach().float()[None]
+    assert rel_inf(out, ref) <= (0 if dtype == torch.float32 else 4e-3)
+    dout = _rand(batch, seq, dim, dtype=dtype, seed=53)
+    out.backward(dout)
+    gW1, gP1 = W.grad.clone(), P.grad.clone()
+    want = torch.zeros(vocab, dim, device=cuda, dtype=torch.float64)
+    want.index_add_(0, tokens.reshape(-1), dout.double().reshape(-1, dim))
+    assert rel_inf(gW1, want) <= (1e-6 if dtype == torch.float32 else 1e-2)
+    assert rel_inf(gP1, dout.double().sum(0)) <= (1e-6 if dtype == torch.float32 else 1e-2)
+    W.grad = None
+    P.grad = None
+    ops.embedding(tokens, W, P).backward(dout)
+    assert torch.equal(W.grad, gW1) and torch.equal(P.grad, gP1)  # bit-reproducible
+
+
+def test_vocab_parallel_embedding_masks_other_ranks(cuda):
+    vocab, dim, tp = 40, 16, 4
+    full = _rand(vocab, dim, dtype=torch.float32, seed=54)
+    tokens = torch.randint(0, vocab, (2, 9), device=cuda)
+    total = torch.zeros(2, 9, dim, device=cuda)
+    for r in range(tp):
+        shard = full[r * 10:(r + 1) * 10].contiguous()
+        total += ops.embedding(tokens, shard, None, vocab_start=r * 10, vocab_rows=10)
+    assert torch.equal(total, F.embedding(tokens, full))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16, torch.int8])
+@pytest.mark.parametrize("shape", [(12, 20), (7, 9), (2048, 512), (3, 1)])
+def test_reshard_cat_and_chunk_bit_exact(cuda, dtype, shape):
+    g = torch.Generator().manual_seed(60)
+    full = (torch.randn(*shape, generator=g) * 100).to(dtype).to(cuda)
+    for dim in (0, 1):
+        for old, new in ((4, 2), (2, 4), (3, 2), (1, 3)):
+            if full.shape[dim] < old:
+                continue
+            shards = [torch.chunk(full, old, dim)[r].contiguous() for r in range(len(torch.chunk(full, old, dim)))]
+            got = reshard.device_cat(shards, dim)
+            assert torch.equal(got, torch.cat(shards, dim))
+            pieces = torch.chunk(full, new, dim)
+            for r in range(len(pieces)):
+                assert torch.equal(reshard.local_slice(full, dim, r, new), pieces[r])
+                assert torch.equal(reshard.repack_shards(shards, dim, r, new), pieces[r])
+
+
+def test_reshard_tp4_to_tp2_layer_at_full_size(cuda):
+    """A d2048 / FFN 8192 layer's column- and row-parallel bf16 shards, TP4 -> TP2, torch.equal."""
+    g = torch.Generator().manual_seed(61)
+    mats = {"q": (2048, 2048, 0), "k": (2048, 2048, 0), "v": (2048, 2048, 0), "out": (2048, 2048, 1),
+            "fc1": (8192, 2048, 0), "fc2": (2048, 8192, 1)}
+    for name, (r, c, dim) in mats.items():
+        full = (torch.randn(r, c, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+        old = [t.contiguous() for t in torch.chunk(full, 4, dim)]
+        for new_rank in range(2):
+            got = reshard.repack_shards(old, dim, new_rank, 2)
+            assert torch.equal(got, torch.chunk(full, 2, dim)[new_rank]), name
+
+
+def test_reshard_unpack_entry_point(cuda):
+    src = torch.arange(6 * 10, dtype=torch.int32, device=cuda).view(6, 10)
+    outs = [torch.empty(6, e, dtype=torch.int32, device=cuda) for e in (3, 3, 4)]
+    ptrs = (ctypes.c_void_p * 3)(*[o.data_ptr() for o in outs])
+    ext = (ctypes.c_int64 * 3)(3, 3, 4)
+    H.call("rh_reshard_unpack", src.data_ptr(), 6, 10, 1, 4, 3, ptrs, ext, H.stream_of(src))
+    for o, want in zip(outs, torch.split(src, [3, 3, 4], 1)):
+        assert torch.equal(o, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_optimizer_steps(cuda, dtype):
+    from resihp.optim import SGD, AdamW
+
+    p0 = _rand(1000, dtype=torch.float32, seed=70)
+    grads = [_rand(1000, dtype=torch.float32, seed=71 + i) for i in range(3)]
+    ours = torch.nn.Parameter(p0.clone().to(dtype))
+    ref = torch.nn.Parameter(p0.clone().to(dtype).float())
+    opt = AdamW([ours], lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    ref_opt = torch.optim.AdamW([ref], lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    for gr in grads:
+        ours.grad = gr.to(dtype)
+        ref.grad = gr.to(dtype).float()
+        opt.step()
+        ref_opt.step()
+    assert rel_inf(ours, ref) <= (1e-6 if dtype == torch.float32 else 4e-3)
+    assert float(opt.state[ours]["step"]) == 3.0
+    s = torch.nn.Parameter(p0.clone().to(dtype))
+    s.grad = grads[0].to(dtype)
+    SGD([s], lr=1e-3).step()
+    assert rel_inf(s, p0.to(dtype).float() - 1e-3 * grads[0].to(dtype).float()) <= (1e-7 if dtype == torch.float32 else 4e-3)

@@ -1,0 +1,234 @@
+"""Model-level parity on the GPU: the reference's golden step, bf16 models, TP shards, 1F1B, reshard.
+
+Bands (north star): fp32 loss and gradients within 1e-5 relative of the reference;
+bf16 within 2e-2 relative of the fp32 oracle on the same (bf16-rounded) weights;
+reshard bit-exact.  "Relative" is the reference's infinity-norm form
+(tests/test_reference.py:154-156): max|a - b| / max|b| per tensor.
+"""
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_inf
+from oracle import torch_ref
+from resihp import ops
+from resihp.config import TrainConfig
+from resihp.model import ReferenceTransformer
+from resihp.optim import SGD
+from resihp.parallel import reshard
+from resihp.parallel.pp import run_1f1b
+from resihp.parallel.tp import TensorParallelStage
+from resihp.reference import next_token_loss, run_reference
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+LAYER = ("attn_norm.weight", "attn_norm.bias", "attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight",
+         "attn.out_proj.weight", "mlp_norm.weight", "mlp_norm.bias", "mlp.fc1.weight", "mlp.fc2.weight")
+
+
+def _cfg1():
+    data = np.load(GOLDEN / "cfg1_step.npz", allow_pickle=False)
+    return data, json.loads(str(data["meta"]))
+
+
+def test_tiny_lm_fp32_step_matches_reference_golden(cuda):
+    """2 layers, d 64, 4 heads, vocab 256, seq 32, batch 4, fp32, seeded reference init: one
+    fwd+bwd+SGD step against the reference's own logits, loss and gradients."""
+    data, meta = _cfg1()
+    c = meta["config"]
+    cfg = TrainConfig(model_dim=c["model_dim"], num_layers=c["num_layers"], num_heads=c["num_heads"],
+                      batch_size=c["batch_size"], micro_batch_size=c["batch_size"], seed=c["seed"], tp=1, pp=1, dp=1,
+                      iterations=1)
+    torch.manual_seed(cfg.seed)
+    model = ReferenceTransformer(cfg, vocab_size=c["vocab"], sequence_length=c["seq"]).to(cuda)
+    tokens = torch.from_numpy(data["tokens"]).to(cuda)
+    logits = model(tokens)
+    loss = next_token_loss(logits, tokens, c["vocab"])
+    loss.backward()
+    assert abs(float(loss) - float(data["loss"])) <= 1e-5 * float(data["loss"])
+    assert rel_inf(logits, torch.from_numpy(data["logits"])) <= 1e-5
+    worst = 0.0
+    for name, p in model.named_parameters():
+        err = rel_inf(p.grad, torch.from_numpy(data["grad/" + name]))
+        worst = max(worst, err)
+        assert err <= 1e-5, (name, err)
+    print(f"worst per-tensor gradient error {worst:.2e}")
+    before = {n: p.detach().clone() for n, p in model.named_parameters()}
+    SGD(model.parameters(), lr=1e-3).step()
+    for name, p in model.named_parameters():
+        want = before[name].cpu() - 1e-3 * torch.from_numpy(data["grad/" + name])
+        assert rel_inf(p, want) <= 1e-6, name
+
+
+def test_reference_run_matches_golden_records(cuda):
+    """The reference suite's config for 3 AdamW iterations: per-step loss within 1e-5."""
+    rec = json.loads((GOLDEN / "ref_records.json").read_text())
+    c = rec["config"]
+    cfg = TrainConfig(model_dim=c["model_dim"], num_layers=c["num_layers"], num_heads=c["num_heads"],
+                      batch_size=c["batch_size"], micro_batch_size=2, seed=c["seed"], tp=2, pp=2, dp=2,
+                      iterations=c["iterations"])
+    records = run_reference(cfg, vocab_size=c["vocab"], sequence_length=c["seq"], device=cuda)
+    for got, want, toks in zip(records, rec["records"], rec["tokens"]):
+        assert [list(r) for r in got.tokens] == toks
+        assert abs(got.loss - want["loss"]) <= 1e-5 * abs(want["loss"]), (got.loss, want["loss"])
+
+
+def _bf16_case(cuda, d=256, heads=4, layers=2, vocab=1000, seq=256, batch=2, seed=3):
+    st = torch_ref.synthetic_state(d, layers, vocab, seq, std=0.02, seed=seed)
+    st = {k: v.to(torch.bfloat16).float() for k, v in st.items()}  # both sides see bf16-exact weights
+    cfg = TrainConfig(model_dim=d, num_layers=layers, num_heads=heads, batch_size=batch, micro_batch_size=batch,
+                      seed=seed, tp=1, pp=1, dp=1, iterations=1)
+    model = ReferenceTransformer(cfg, vocab_size=vocab, sequence_length=seq)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            p.copy_(st[n])
+    model = model.to(cuda, torch.bfloat16)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=torch.Generator().manual_seed(seed))
+    return st, model, tokens
+
+
+def test_bf16_lm_matches_fp32_oracle(cuda):
+    st, model, tokens = _bf16_case(cuda)
+    logits = model(tokens.to(cuda))
+    loss = next_token_loss(logits, tokens.to(cuda), 1000)
+    loss.backward()
+    ref_logits, ref_loss, ref_grads = torch_ref.loss_and_grads(st, tokens, 4, range(2), 1000)
+    assert abs(float(loss) - float(ref_loss)) <= 2e-2 * float(ref_loss)
+    assert rel_inf(logits, ref_logits) <= 2e-2
+    for name, p in model.named_parameters():
+        assert rel_inf(p.grad, ref_grads[name]) <= 2e-2, (name, rel_inf(p.grad, ref_grads[name]))
+
+
+def _shard_block_inputs(cuda, d, heads_total, tp, rank, seq, batch, seed):
+    full = torch_ref.synthetic_state(d, 1, 8, seq, std=0.02, seed=seed, first=False, last=False)
+    full = {k: v.to(torch.bfloat16) for k, v in full.items()}
+    layout = reshard.shard_dims([0])
+    local = {k: torch_ref.local_slice(v, layout[k], rank, tp) for k, v in full.items()}
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(batch, seq, d, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(batch, seq, d, generator=g) * 1e-2).to(torch.bfloat16)
+    return local, x, dy
+
+
+@pytest.mark.parametrize("d,heads,tp,rank,seq,batch", [
+    (2048, 16, 4, 2, 2048, 4),   # one TP=4 rank of a GPT-1.3B-shape block
+    (512, 8, 2, 1, 384, 2),
+])
+def test_shard_block_matches_fp32_reference(cuda, d, heads, tp, rank, seq, batch):
+    local, x, dy = _shard_block_inputs(cuda, d, heads, tp, rank, seq, batch, seed=11)
+    cfg = TrainConfig(model_dim=d, num_layers=1, num_heads=heads, batch_size=batch, micro_batch_size=batch, seed=0,
+                      tp=tp, pp=1, dp=1, iterations=1)
+    stage = TensorParallelStage(cfg, vocab_size=8 * tp, sequence_length=seq, layer_ids=[0], is_first=False,
+                                is_last=False, local_state={k: v.to(cuda) for k, v in local.items()},
+                                tp_rank=rank, tp_size=tp)
+    xg = x.to(cuda).requires_grad_(True)
+    out = stage(hidden=xg)
+    out.backward(dy.to(cuda))
+    # fp32 torch reference of the same shard math on the GPU
+    ref_p = {k: v.to(cuda).float().requires_grad_(True) for k, v in local.items()}
+    xr = x.to(cuda).float().requires_grad_(True)
+    ref = torch_ref.shard_forward(ref_p, num_heads=heads, tp_rank=rank, tp_size=tp, vocab_size=8 * tp,
+                                  layer_ids=[0], is_first=False, is_last=False, hidden=xr)
+    ref.backward(dy.to(cuda).float())
+    assert rel_inf(out, ref) <= 2e-2
+    assert rel_inf(xg.grad, xr.grad) <= 2e-2
+    for name, (p, _) in stage.local_shards().items():
+        err = rel_inf(p.grad, ref_p[name].grad)
+        assert err <= 2e-2, (name, err)
+
+
+def test_tp1_stage_is_bitwise_the_model(cuda):
+    torch.manual_seed(5)
+    cfg = TrainConfig(model_dim=64, num_layers=2, num_heads=4, batch_size=2, micro_batch_size=2, seed=5, tp=1, pp=1,
+                      dp=1, iterations=1)
+    model = ReferenceTransformer(cfg, vocab_size=128, sequence_length=32).to(cuda)
+    local = reshard.shard_logical_state(model.logical_state_dict(), layout=reshard.shard_dims(range(2)), tp_rank=0,
+                                        tp_size=1)
+    stage = TensorParallelStage(cfg, vocab_size=128, sequence_length=32, layer_ids=range(2), is_first=True,
+                                is_last=True, local_state=local, tp_rank=0, tp_size=1)
+    tokens = torch.randint(0, 128, (2, 32), device=cuda)
+    a, b = model(tokens), stage(tokens=tokens)
+    assert torch.equal(a, b)
+    next_token_loss(a, tokens, 128).backward()
+    next_token_loss(b, tokens, 128).backward()
+    for name, (p, _) in stage.local_shards().items():
+        assert torch.equal(p.grad, model.logical_state_dict()[name].grad), name
+
+
+def test_1f1b_order_and_accumulation(cuda):
+    """Stage 1 of 4 running 8 micro-batches: the reference's 1F1B order, and gradients that equal
+    running the micro-batches one after another."""
+    d, heads, seq, mb = 128, 4, 64, 2
+    cfg = TrainConfig(model_dim=d, num_layers=6, num_heads=heads, batch_size=16, micro_batch_size=mb, seed=0,
+                      tp=1, pp=4, dp=1, iterations=1)
+    full = torch_ref.synthetic_state(d, 6, 8, seq, std=0.02, seed=2, first=False, last=False, layer_ids=range(6))
+    local = {k: v.to(cuda, torch.bfloat16) for k, v in full.items()}
+    g = torch.Generator().manual_seed(4)
+    xs = [torch.randn(mb, seq, d, generator=g).to(cuda, torch.bfloat16) for _ in range(8)]
+    dys = [(torch.randn(mb, seq, d, generator=g) * 1e-2).to(cuda, torch.bfloat16) for _ in range(8)]
+
+    def stage():
+        return TensorParallelStage(cfg, vocab_size=8, sequence_length=seq, layer_ids=range(6), is_first=False,
+                                   is_last=False, local_state=local, tp_rank=0, tp_size=1)
+
+    s1 = stage()
+    inputs = [x.clone().requires_grad_(True) for x in xs]
+    order, _ = run_1f1b(s1, stage_index=1, num_stages=4, inputs=inputs, grads=dys)
+    assert order == torch_ref.issue_order(8, 1, 4)
+    s2 = stage()
+    for x, dy in zip(xs, dys):
+        s2(hidden=x.clone().requires_grad_(True)).backward(dy)
+    for (n, (p1, _)), (_, (p2, _)) in zip(s1.local_shards().items(), s2.local_shards().items()):
+        assert torch.equal(p1.grad, p2.grad), n
+
+
+def test_reshard_then_step_tp4_to_tp2(cuda):
+    """A d2048 / FFN 8192 layer's TP4 shards re-sliced on the device into TP2 rank 1, bit-exact,
+    then that rank's fwd+bwd at seq 2048, micro-batch 2 against the fp32 reference."""
+    d, heads, seq, batch = 2048, 16, 2048, 2
+    full = torch_ref.synthetic_state(d, 1, 8, seq, std=0.02, seed=21, first=False, last=False)
+    full = {k: v.to(cuda, torch.bfloat16) for k, v in full.items()}
+    layout = reshard.shard_dims([0])
+    old = {k: [reshard.local_slice(v, layout[k], r, 4) for r in range(4)] for k, v in full.items()}
+    new = {k: reshard.repack_shards(old[k], layout[k], 1, 2) for k in full}
+    for k, v in full.items():
+        want = v if layout[k] is None else torch.chunk(v, 2, layout[k])[1]
+        assert torch.equal(new[k], want), k
+    cfg = TrainConfig(model_dim=d, num_layers=1, num_heads=heads, batch_size=batch, micro_batch_size=batch, seed=0,
+                      tp=2, pp=1, dp=1, iterations=1)
+    stage = TensorParallelStage(cfg, vocab_size=16, sequence_length=seq, layer_ids=[0], is_first=False,
+                                is_last=False, local_state=new, tp_rank=1, tp_size=2)
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(batch, seq, d, generator=g).to(cuda, torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn(batch, seq, d, generator=g) * 1e-2).to(cuda, torch.bfloat16)
+    out = stage(hidden=x)
+    out.backward(dy)
+    ref_p = {k: v.float().requires_grad_(True) for k, v in new.items()}
+    xr = x.detach().float().requires_grad_(True)
+    ref = torch_ref.shard_forward(ref_p, num_heads=heads, tp_rank=1, tp_size=2, vocab_size=16, layer_ids=[0],
+                                  is_first=False, is_last=False, hidden=xr)
+    ref.backward(dy.float())
+    assert rel_inf(out, ref) <= 2e-2
+    assert rel_inf(x.grad, xr.grad) <= 2e-2
+    for name, (p, _) in stage.local_shards().items():
+        assert rel_inf(p.grad, ref_p[name].grad) <= 2e-2, name
+
+
+def test_block_backward_is_deterministic(cuda):
+    local, x, dy = _shard_block_inputs(cuda, 512, 8, 1, 0, 512, 2, seed=31)
+    params = [torch.nn.Parameter(local["layers.0." + n].to(cuda)) for n in LAYER]
+    grads = []
+    for _ in range(2):
+        for p in params:
+            p.grad = None
+        xg = x.to(cuda).requires_grad_(True)
+        ops.transformer_block(xg, *params, 8).backward(dy.to(cuda))
+        grads.append([xg.grad.clone()] + [p.grad.clone() for p in params])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
