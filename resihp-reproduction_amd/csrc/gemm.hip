@@ -1,22 +1,37 @@
 // Dense GEMMs of the decoder block (F.linear and its backward) for gfx950.
 //
-// bf16 path: 128x128x64 workgroup tile, 4 waves in a 2x2 grid, each wave a
-// 64x64 sub-tile built from v_mfma_f32_16x16x32_bf16 (fp32 accumulators).
-// Both operands are staged through LDS in a k-contiguous layout
-// ([rows][BK+8], the +8 pad keeps the 16-byte fragment reads of 16 lanes on
-// distinct banks) and double-buffered: the global loads of tile k+1 are issued
-// before the MFMAs of tile k and written to the other LDS buffer afterwards,
-// so one barrier per k-tile suffices.  Operands whose memory layout is
-// m/n-contiguous (dgrad's weight, both wgrad operands) are transposed while
-// being written to LDS.
+// bf16 path (MFMA).  Workgroup tiles of BM x BN x 64 built from
+// v_mfma_f32_32x32x16_bf16 (the 32x32 form: ~2.2 PFLOP/s sustained on MI355X,
+// the 16x16x32 form reaches barely half that).  Three tile shapes:
+//   256x256, 8 waves (2x4, 128x64 per wave)   -- large outputs
+//   256x128, 8 waves (4x2,  64x64 per wave)   -- medium
+//   128x128, 4 waves (2x2,  64x64 per wave)   -- small / split-K
+// chosen per call by the number of tiles against the CU count.
 //
-// fp32 path: 64x64x16 FMA tile (4x4 outputs per thread).  Used for the fp32
-// parity mode, where no bf16 rounding may enter.
+// Operands are staged through LDS, double-buffered (global loads of k-tile
+// t+1 are in flight while the MFMAs of tile t run; one barrier per k-tile):
+//   k-contiguous operand  (A of NT/NN, B of NT): LDS [rows][64], 128-byte rows,
+//     16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7), so the 16
+//     rows a ds_read_b128 phase touches hit 16 distinct bank groups;
+//   m/n-contiguous operand (A of TN, B of NN/TN): LDS [64][cols] exactly as in
+//     memory (16-byte stores), 32-element unit u of row k stored at u ^ (k & 3),
+//     and MFMA fragments are read with ds_read_b64_tr_b16: in each 16-lane
+//     block, lane i addresses row k0 + i/4, columns c0 + 4*(i%4) .. +3, and lane
+//     j receives rows k0..k0+3 of column c0 + j -- a k-major fragment without
+//     any scalar transposition.
+// Workgroup ids are remapped so that each XCD (ids are dealt round-robin over
+// the 8 XCDs) works on one contiguous run of a GROUP_M-grouped tile order:
+// tiles sharing A rows / B columns land in the same XCD's L2.
 //
-// Split-K: when the output has fewer tiles than the chip has CUs and K is
-// long (the wgrad shapes), grid.z partitions K, every split writes fp32
-// partials to the caller's workspace, and a reduce kernel sums them in split
-// order (deterministic) and applies the epilogue.
+// fp32 path: 64x64x16 FMA tile (4x4 outputs per thread) for the fp32 parity
+// mode, where no bf16 rounding may enter.
+//
+// Split-K: when the output has too few tiles for the chip and K is long (the
+// wgrad shapes), grid.z partitions K, each split writes fp32 partials to the
+// caller's workspace, and a reduce kernel sums them in split order
+// (deterministic) and applies the epilogue.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "common.hpp"
@@ -24,6 +39,9 @@
 int rh_device_cus();
 
 namespace {
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 template <typename T>
 struct GemmParams {
@@ -47,6 +65,7 @@ struct GemmParams {
   float* ws;            // split-K partials [splits][M][N]
   int64_t k_per_split;  // multiple of the k-tile
   int aligned;          // all rows 16-byte aligned -> vector loads
+  int tiles_m, tiles_n, group_m;
 };
 
 template <typename T>
@@ -80,29 +99,52 @@ __device__ __forceinline__ void epilogue_store(const GemmParams<T>& p, int64_t m
   st_f32(drow + n, v);
 }
 
+// XCD-aware, GROUP_M-grouped tile coordinates of this workgroup.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int nwg = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  const int q = nwg / 8, r = nwg % 8;
+  const int xcd = bid % 8, idx = bid / 8;
+  const int logical = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + idx;
+  const int per_group = group_m * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int in = logical - g * per_group;
+  tm = first_m + in % gsize;
+  tn = in / gsize;
+}
+
 // ---------------------------------------------------------------------------
 // bf16 MFMA kernel
 // ---------------------------------------------------------------------------
-constexpr int kBM = 128, kBN = 128, kBK = 64, kPad = 8, kLdsP = kBK + kPad;
+constexpr int kBK = 64;
 
-// One operand tile of ROWS (m or n) x BK, loaded from global into registers
-// and written to LDS as s[row][k].
-//   KC = true : global row r is k-contiguous: element (r, k) = rowptr(r)[k]
-//   KC = false: global row k is r-contiguous: element (r, k) = rowptr(k)[r]
-template <int ROWS, bool KC>
+// element offset of (row r, 16-byte chunk c) in a k-contiguous [R][64] tile
+__device__ __forceinline__ int kc_off(int r, int c) { return r * kBK + ((c ^ ((r >> 1) & 7)) << 3); }
+// element offset of (k row, column col) in an m/n-contiguous [64][R] tile
+template <int R>
+__device__ __forceinline__ int mc_off(int k, int col) {
+  return k * R + ((((col >> 5) ^ (k & 3))) << 5) + (col & 31);
+}
+
+// One operand tile (ROWS = m or n extent, 64 k), global -> registers -> LDS.
+//   KC: global row r is k-contiguous: element (r, k) = rowptr(r)[k]
+//   !KC: global row k is r-contiguous: element (r, k) = rowptr(k)[r]
+template <int ROWS, bool KC, int NT>
 struct TileIO {
   static constexpr int kChunks = ROWS * kBK / 8;
-  static constexpr int kPer = kChunks / 256;
+  static constexpr int kPer = kChunks / NT;
+  static_assert(kChunks % NT == 0, "tile must split evenly over the threads");
   u16x8_t reg[kPer];
 
-  // `outer_lim` bounds the row index (M or N), `k_lim` bounds k.
   template <typename RowFn>
   __device__ __forceinline__ void load(RowFn rowptr, int64_t o0, int64_t k0, int64_t outer_lim, int64_t k_lim,
-                                       bool aligned) {
+                                       bool fast, bool aligned) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + i * 256;
-      int64_t r, k;  // first element of the chunk
+      const int c = threadIdx.x + i * NT;
+      int64_t r, k;
       if (KC) {
         r = o0 + c / (kBK / 8);
         k = k0 + (c % (kBK / 8)) * 8;
@@ -111,7 +153,9 @@ struct TileIO {
         r = o0 + (c % (ROWS / 8)) * 8;
       }
       u16x8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (KC) {
+      if (fast) {
+        v = *reinterpret_cast<const u16x8_t*>(KC ? rowptr(r) + k : rowptr(k) + r);
+      } else if (KC) {
         if (r < outer_lim && k < k_lim) {
           const bf16_t* src = rowptr(r) + k;
           if (aligned && k + 8 <= k_lim) {
@@ -138,111 +182,276 @@ struct TileIO {
     }
   }
 
-  __device__ __forceinline__ void store(bf16_t (*s)[kLdsP]) {
+  __device__ __forceinline__ void store(bf16_t* s) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + i * 256;
+      const int c = threadIdx.x + i * NT;
       if (KC) {
-        const int r = c / (kBK / 8), k = (c % (kBK / 8)) * 8;
-        *reinterpret_cast<u16x8_t*>(&s[r][k]) = reg[i];
+        const int r = c / (kBK / 8), ch = c % (kBK / 8);
+        *reinterpret_cast<u16x8_t*>(s + kc_off(r, ch)) = reg[i];
       } else {
-        const int k = c / (ROWS / 8), r = (c % (ROWS / 8)) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s[r + j][k] = reg[i][j];
+        const int k = c / (ROWS / 8), col = (c % (ROWS / 8)) * 8;
+        *reinterpret_cast<u16x8_t*>(s + mc_off<ROWS>(k, col)) = reg[i];
       }
     }
   }
 };
 
-template <int L, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void gemm_bf16_mfma(GemmParams<bf16_t> p) {
+// MFMA fragment (32 rows/cols starting at rb, k-step ks) from an LDS tile.
+template <int ROWS, bool KC>
+__device__ __forceinline__ bf16x8_t load_frag(const bf16_t* s, int rb, int ks, int lane) {
+  if (KC) {
+    const int r = rb + (lane & 31);
+    return *reinterpret_cast<const bf16x8_t*>(s + kc_off(r, ks * 2 + (lane >> 5)));
+  } else {
+    const int q = lane >> 4, i = lane & 15;
+    const int col = rb + 16 * (q & 1) + 4 * (i & 3);
+    const int k = ks * 16 + 8 * (q >> 1) + (i >> 2);
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(s + mc_off<ROWS>(k, col)));
+    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(s + mc_off<ROWS>(k + 4, col)));
+    s16x4_t both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8_t, both);
+  }
+}
+
+// Interior-tile operand loader: every chunk in bounds and 16-byte aligned, per-thread
+// pointers set up once; one k-tile advance is a pointer add (k-contiguous) or a
+// scalar row-base computation (m/n-contiguous, where a k-tile never straddles a
+// q/k/v segment).
+template <int ROWS, bool KC, int NT>
+struct FastIO {
+  static constexpr int kChunks = ROWS * kBK / 8;
+  static constexpr int kPer = kChunks / NT;
+  u16x8_t reg[kPer];
+  const bf16_t* ptr[kPer];  // KC: chunk pointers at k = kbeg
+  int64_t off[kPer];        // !KC: element offset of each chunk from its k-tile's first row
+
+  template <typename RowFn>
+  __device__ __forceinline__ void setup(RowFn rowptr, int64_t o0, int64_t kbeg, int64_t ld) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (KC) {
+        ptr[i] = rowptr(o0 + c / (kBK / 8)) + kbeg + (c % (kBK / 8)) * 8;
+      } else {
+        off[i] = (int64_t)(c / (ROWS / 8)) * ld + o0 + (c % (ROWS / 8)) * 8;
+      }
+    }
+  }
+
+  // k-tile starting at k0 (= kbeg + kt*kBK); `base` is the row pointer of row k0 (!KC only)
+  __device__ __forceinline__ void load(int kt, const bf16_t* base) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      reg[i] = KC ? *reinterpret_cast<const u16x8_t*>(ptr[i] + (int64_t)kt * kBK)
+                  : *reinterpret_cast<const u16x8_t*>(base + off[i]);
+  }
+
+  __device__ __forceinline__ void store(bf16_t* s) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (KC) {
+        *reinterpret_cast<u16x8_t*>(s + kc_off(c / (kBK / 8), c % (kBK / 8))) = reg[i];
+      } else {
+        *reinterpret_cast<u16x8_t*>(s + mc_off<ROWS>(c / (ROWS / 8), (c % (ROWS / 8)) * 8)) = reg[i];
+      }
+    }
+  }
+};
+
+template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC, int FM, int FN>
+__device__ __forceinline__ void mma_ktile(const bf16_t* a_s, const bf16_t* b_s, floatx16_t (&acc)[FM][FN], int wm,
+                                          int wn, int lane) {
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
+    bf16x8_t af[FM], bfr[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[i] = load_frag<BM, A_KC>(a_s, wm * WTM + i * 32, ks, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[j] = load_frag<BN, B_KC>(b_s, wn * WTN + j * 32, ks, lane);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16_t> p) {
+  constexpr int NT = 64 * WGM * WGN;
   constexpr bool A_KC = (L != RH_GEMM_TN);
   constexpr bool B_KC = (L == RH_GEMM_NT);
-  constexpr int WTM = kBM / 2, WTN = kBN / 2, FM = WTM / 16, FN = WTN / 16;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK, STAGE = A_ELEMS + B_ELEMS;
 
-  __shared__ __attribute__((aligned(16))) bf16_t sA[2][kBM][kLdsP];
-  __shared__ __attribute__((aligned(16))) bf16_t sB[2][kBN][kLdsP];
+  // two stages, each [A tile | B tile]
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
 
-  const int64_t tiles_n = (p.N + kBN - 1) / kBN;
-  const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
-  const int64_t m0 = tm * kBM, n0 = tn * kBN;
+  int tm, tn;
+  tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t kbeg = (int64_t)blockIdx.z * p.k_per_split;
   const int64_t kend = min(p.K, kbeg + p.k_per_split);
   const int nk = (int)((kend - kbeg + kBK - 1) / kBK);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const bool aligned = p.aligned != 0;
+  // interior: no bounds checks, 16-byte loads, and (for a segmented m/n-contiguous B) every
+  // k-tile inside one segment
+  const bool interior = aligned && m0 + BM <= p.M && n0 + BN <= p.N && (kend - kbeg) % kBK == 0 &&
+                        (B_KC || p.b_nseg == 1 || p.b_seg % kBK == 0);
 
-  auto a_row = [&](int64_t r) -> const bf16_t* { return p.A + r * p.lda; };
-  auto bb_row = [&](int64_t r) -> const bf16_t* { return b_row(p, r); };
-
-  TileIO<kBM, A_KC> ta;
-  TileIO<kBN, B_KC> tb;
-
-  floatx4_t acc[FM][FN];
+  floatx16_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  if (nk > 0) {
-    ta.load(a_row, m0, kbeg, p.M, kend, aligned);
-    tb.load(bb_row, n0, kbeg, p.N, kend, aligned);
-    ta.store(sA[0]);
-    tb.store(sB[0]);
-  }
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = (kt + 1) < nk;
-    if (more) {
-      const int64_t k0 = kbeg + (int64_t)(kt + 1) * kBK;
-      ta.load(a_row, m0, k0, p.M, kend, aligned);
-      tb.load(bb_row, n0, k0, p.N, kend, aligned);
+  if (interior) {
+    FastIO<BM, A_KC, NT> fa;
+    FastIO<BN, B_KC, NT> fb;
+    fa.setup([&](int64_t r) { return p.A + r * p.lda; }, m0, kbeg, p.lda);
+    fb.setup([&](int64_t r) { return b_row(p, r); }, n0, kbeg, p.ldb);
+    // row-k base pointers of the m/n-contiguous operands (one scalar lookup per k-tile)
+    auto a_base = [&](int kt) -> const bf16_t* { return A_KC ? nullptr : p.A + (kbeg + (int64_t)kt * kBK) * p.lda; };
+    auto b_base = [&](int kt) -> const bf16_t* { return B_KC ? nullptr : b_row(p, kbeg + (int64_t)kt * kBK); };
+    if (nk > 0) {
+      fa.load(0, a_base(0));
+      fb.load(0, b_base(0));
+      fa.store(smem);
+      fb.store(smem + A_ELEMS);
     }
-#pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      bf16x8_t af[FM], bfr[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(&sA[cur][wm * WTM + i * 16 + (lane & 15)][ks * 32 + (lane >> 4) * 8]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(&sB[cur][wn * WTN + j * 16 + (lane & 15)][ks * 32 + (lane >> 4) * 8]);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = (kt + 1) < nk;
+      if (more) {
+        fa.load(kt + 1, a_base(kt + 1));
+        fb.load(kt + 1, b_base(kt + 1));
+      }
+      const bf16_t* a_s = smem + cur * STAGE;
+      mma_ktile<BM, BN, WGM, WGN, A_KC, B_KC, FM, FN>(a_s, a_s + A_ELEMS, acc, wm, wn, lane);
+      if (more) {
+        bf16_t* nxt = smem + (cur ^ 1) * STAGE;
+        fa.store(nxt);
+        fb.store(nxt + A_ELEMS);
+      }
+      __syncthreads();
+    }
+  } else {
+    auto a_row = [&](int64_t r) -> const bf16_t* { return p.A + r * p.lda; };
+    auto bb_row = [&](int64_t r) -> const bf16_t* { return b_row(p, r); };
+    TileIO<BM, A_KC, NT> ta;
+    TileIO<BN, B_KC, NT> tb;
+    if (nk > 0) {
+      ta.load(a_row, m0, kbeg, p.M, kend, false, aligned);
+      tb.load(bb_row, n0, kbeg, p.N, kend, false, aligned);
+      ta.store(smem);
+      tb.store(smem + A_ELEMS);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = (kt + 1) < nk;
+      if (more) {
+        const int64_t k0 = kbeg + (int64_t)(kt + 1) * kBK;
+        ta.load(a_row, m0, k0, p.M, kend, false, aligned);
+        tb.load(bb_row, n0, k0, p.N, kend, false, aligned);
+      }
+      const bf16_t* a_s = smem + cur * STAGE;
+      mma_ktile<BM, BN, WGM, WGN, A_KC, B_KC, FM, FN>(a_s, a_s + A_ELEMS, acc, wm, wn, lane);
+      if (more) {
+        bf16_t* nxt = smem + (cur ^ 1) * STAGE;
+        ta.store(nxt);
+        tb.store(nxt + A_ELEMS);
+      }
+      __syncthreads();
+    }
+  }
+
+  // Epilogue through LDS: the fp32 tile is written to LDS in row chunks, then every thread
+  // takes 8 consecutive columns at a time -- one rolled loop, 16-byte coalesced loads and
+  // stores.  32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
+  // column l%32.
+  constexpr int CP = BN >= 256 ? BN : BN + 4;                 // fp32 row pitch in LDS
+  constexpr int CH_MAX = (2 * STAGE * (int)sizeof(bf16_t)) / (CP * 4);
+  constexpr int CH = CH_MAX >= BM ? BM : (CH_MAX >= WTM ? (CH_MAX / WTM) * WTM : WTM);
+  static_assert(CH * CP * 4 <= 2 * STAGE * (int)sizeof(bf16_t), "epilogue chunk must fit the LDS stages");
+  float* cs = reinterpret_cast<float*>(smem);
+  const int g = lane >> 5, c32 = lane & 31;
+  for (int r0 = 0; r0 < BM; r0 += CH) {
+    // waves whose rows fall in [r0, r0 + CH) deposit their accumulators
+    if (wm * WTM >= r0 && wm * WTM < r0 + CH) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      ta.store(sA[cur ^ 1]);
-      tb.store(sB[cur ^ 1]);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * WTM - r0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            cs[row * CP + wn * WTN + j * 32 + c32] = acc[i][j][r];
+          }
     }
     __syncthreads();
-  }
-
-  // Output fragment (i, j), register r of lane l holds
-  //   row = 16*i + 4*(l/16) + r, col = 16*j + l%16   of the wave's sub-tile.
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t m = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-      if (m >= p.M) continue;
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + wn * WTN + j * 16 + (lane & 15);
-        if (n >= p.N) continue;
-        if (SPLIT) {
-          p.ws[(int64_t)blockIdx.z * p.M * p.N + m * p.N + n] = acc[i][j][r];
+#pragma unroll 1
+    for (int e = threadIdx.x; e < CH * (BN / 8); e += NT) {
+      const int row = e / (BN / 8), col = (e % (BN / 8)) * 8;
+      const int64_t m = m0 + r0 + row, n = n0 + col;
+      if (m >= p.M || n >= p.N) continue;
+      const floatx4_t lo = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col);
+      const floatx4_t hi = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col + 4);
+      float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if (SPLIT) {
+        float* w = p.ws + (int64_t)blockIdx.z * p.M * p.N + m * p.N + n;
+        if (n + 8 <= p.N && p.N % 4 == 0) {
+          *reinterpret_cast<floatx4_t*>(w) = lo;
+          *reinterpret_cast<floatx4_t*>(w + 4) = hi;
         } else {
-          epilogue_store<bf16_t, EPI>(p, m, n, acc[i][j][r]);
+          for (int t = 0; t < 8 && n + t < p.N; ++t) w[t] = v[t];
         }
+        continue;
+      }
+      bf16_t* dp = d_row(p, m) + n;
+      const bf16_t* cp = p.C ? p.C + m * p.ldc + n : dp;
+      const bf16_t* xp = EPI == RH_EPI_GELU ? p.aux_out + m * p.ldaux + n
+                                            : (EPI == RH_EPI_GELU_GRAD ? p.aux + m * p.ldaux + n : dp);
+      const bool vec = n + 8 <= p.N && (((uintptr_t)dp | (uintptr_t)xp) & 15) == 0 &&
+                       (p.beta == 0.f || ((uintptr_t)cp & 15) == 0);
+      if (vec) {
+        if (p.beta != 0.f) {
+          const u16x8_t c = *reinterpret_cast<const u16x8_t*>(cp);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = p.alpha * v[t] + p.beta * bf16_to_f32(c[t]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
+        }
+        u16x8_t o;
+        if (EPI == RH_EPI_GELU) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+          *reinterpret_cast<u16x8_t*>(const_cast<bf16_t*>(xp)) = o;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
+        } else if (EPI == RH_EPI_GELU_GRAD) {
+          const u16x8_t a = *reinterpret_cast<const u16x8_t*>(xp);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+        *reinterpret_cast<u16x8_t*>(dp) = o;
+      } else {
+        for (int t = 0; t < 8 && n + t < p.N; ++t) epilogue_store<bf16_t, EPI>(p, m, n + t, v[t]);
       }
     }
+    __syncthreads();
   }
 }
 
@@ -330,34 +539,66 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams<T> p, int s
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+enum TileCfg { kT256x256 = 0, kT256x128 = 1, kT128x128 = 2, kTf32 = 3 };
+
+struct TileShape {
+  int bm, bn, threads;
+};
+constexpr TileShape kShapes[4] = {{256, 256, 512}, {256, 128, 512}, {128, 128, 256}, {fBM, fBN, 256}};
+
 struct Plan {
+  int cfg;
   int splits;
   int64_t k_per_split;
   int64_t ws_bytes;
+  int tiles_m, tiles_n;
 };
 
+// Relative throughput of one CU on each tile shape (measured order of magnitude; bigger
+// tiles re-read less of A and B per FLOP).
+constexpr double kTileEff[3] = {1.0, 0.85, 0.6};
+
 Plan plan_gemm(const rh_gemm_desc* d) {
-  Plan pl{1, d->K, 0};
-  const bool bf16 = d->dtype == RH_DTYPE_BF16;
-  const int64_t bm = bf16 ? kBM : fBM, bn = bf16 ? kBN : fBN, bk = bf16 ? kBK : fBK;
-  const int64_t tiles = rh_cdiv(d->M, bm) * rh_cdiv(d->N, bn);
+  Plan pl{kTf32, 1, 0, 0, 0, 0};
+  if (d->dtype != RH_DTYPE_BF16) {
+    pl.tiles_m = (int)rh_cdiv(d->M, fBM);
+    pl.tiles_n = (int)rh_cdiv(d->N, fBN);
+    pl.k_per_split = rh_cdiv(d->K, fBK) * fBK;
+    return pl;
+  }
   const int64_t cus = rh_device_cus();
-  if (!bf16 || d->K < 1024 || tiles >= cus) {
-    pl.k_per_split = rh_cdiv(d->K, bk) * bk;
-    return pl;
+  // RESIHP_GEMM_TILE=0/1/2 pins the tile shape (256x256 / 256x128 / 128x128); tests use it to
+  // run every shape on every layout.
+  int only = -1;
+  if (const char* e = getenv("RESIHP_GEMM_TILE")) {
+    if (e[0] >= '0' && e[0] <= '2' && e[1] == 0) only = e[0] - '0';
   }
-  int64_t splits = rh_cdiv(2 * cus, tiles);
-  if (splits > 8) splits = 8;
-  int64_t kps = rh_cdiv(rh_cdiv(d->K, splits), bk) * bk;
-  if (kps < 512) kps = 512;
-  splits = rh_cdiv(d->K, kps);
-  if (splits <= 1) {
-    pl.k_per_split = rh_cdiv(d->K, bk) * bk;
-    return pl;
+  // estimated time ~ (tiles resident per CU over the whole run) x tile area x k / efficiency;
+  // split K when one wave of tiles leaves CUs idle
+  double best = 1e300;
+  for (int c = 0; c < 3; ++c) {
+    if (only >= 0 && c != only) continue;
+    const int64_t tm = rh_cdiv(d->M, kShapes[c].bm), tn = rh_cdiv(d->N, kShapes[c].bn);
+    const int64_t tiles = tm * tn;
+    const int64_t per_cu = c == kT128x128 ? 2 : 1;  // co-resident workgroups (LDS-bound)
+    const int64_t slots = cus * per_cu;
+    for (int64_t splits = 1; splits <= 8; splits *= 2) {
+      if (splits > 1 && (d->K / splits < 512 || tiles * (splits / 2) >= slots)) break;
+      const int64_t kps = rh_cdiv(rh_cdiv(d->K, splits), kBK) * kBK;
+      const int64_t waves = rh_cdiv(tiles * splits, slots);
+      double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / kTileEff[c];
+      if (splits > 1) t += 4.0 * (double)splits * d->M * d->N / 64.0;  // partial write + reduce traffic
+      if (t < best * 0.98) {
+        best = t;
+        pl.cfg = c;
+        pl.splits = (int)rh_cdiv(d->K, kps);
+        pl.k_per_split = kps;
+        pl.tiles_m = (int)tm;
+        pl.tiles_n = (int)tn;
+      }
+    }
   }
-  pl.splits = (int)splits;
-  pl.k_per_split = kps;
-  pl.ws_bytes = splits * d->M * d->N * (int64_t)sizeof(float);
+  pl.ws_bytes = pl.splits > 1 ? (int64_t)pl.splits * d->M * d->N * (int64_t)sizeof(float) : 0;
   return pl;
 }
 
@@ -369,16 +610,15 @@ int validate(const rh_gemm_desc* d) {
              d->epilogue);
   RH_REQUIRE(d->M >= 0 && d->N >= 0 && d->K >= 0, "rh_gemm: negative extent M=%lld N=%lld K=%lld",
              (long long)d->M, (long long)d->N, (long long)d->K);
+  RH_REQUIRE(d->M <= INT32_MAX / 2 && d->N <= INT32_MAX / 2, "rh_gemm: M or N too large");
   RH_REQUIRE(d->b_nseg >= 1 && d->b_nseg <= RH_MAX_SEG && d->d_nseg >= 1 && d->d_nseg <= RH_MAX_SEG,
              "rh_gemm: segment count out of range (b %d, d %d)", d->b_nseg, d->d_nseg);
   if (d->M == 0 || d->N == 0) return RH_OK;
   RH_REQUIRE(d->A || d->K == 0, "rh_gemm: null A");
   RH_REQUIRE(d->D[0], "rh_gemm: null D");
-  const int64_t a_rows = d->layout == RH_GEMM_TN ? d->K : d->M;
   const int64_t a_cols = d->layout == RH_GEMM_TN ? d->M : d->K;
   const int64_t b_rows = d->layout == RH_GEMM_NT ? d->N : d->K;
   const int64_t b_cols = d->layout == RH_GEMM_NT ? d->K : d->N;
-  (void)a_rows;
   RH_REQUIRE(d->lda >= a_cols, "rh_gemm: lda %lld < %lld", (long long)d->lda, (long long)a_cols);
   RH_REQUIRE(d->ldb >= b_cols, "rh_gemm: ldb %lld < %lld", (long long)d->ldb, (long long)b_cols);
   RH_REQUIRE(d->ldd >= d->N, "rh_gemm: ldd %lld < N %lld", (long long)d->ldd, (long long)d->N);
@@ -425,18 +665,36 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   p.aux = static_cast<const T*>(d->aux); p.aux_out = static_cast<T*>(d->aux_out); p.ldaux = d->ldaux;
   p.ws = static_cast<float*>(ws);
   p.k_per_split = pl.k_per_split;
-  bool al = true;
   const int64_t vec = 16 / (int64_t)sizeof(T);
-  al = al && rh_aligned(d->A, 16) && d->lda % vec == 0 && d->ldb % vec == 0;
+  bool al = rh_aligned(d->A, 16) && d->lda % vec == 0 && d->ldb % vec == 0;
   for (int s = 0; s < d->b_nseg; ++s) al = al && rh_aligned(d->B[s], 16);
+  // segment boundaries must not split a 16-byte chunk of the k-contiguous B or a k-tile row
+  if (d->b_nseg > 1) al = al && d->b_seg_rows % 8 == 0;
   p.aligned = al ? 1 : 0;
+  p.tiles_m = pl.tiles_m;
+  p.tiles_n = pl.tiles_n;
+  p.group_m = 8;
   return p;
 }
 
+template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
+void launch_bf16(const GemmParams<bf16_t>& p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
+}
+
+template <int L, int EPI, bool SPLIT>
+void launch_cfg(int cfg, const GemmParams<bf16_t>& p, dim3 grid, hipStream_t st) {
+  switch (cfg) {
+    case kT256x256: launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, grid, st); break;
+    case kT256x128: launch_bf16<256, 128, 4, 2, L, EPI, SPLIT>(p, grid, st); break;
+    default: launch_bf16<128, 128, 2, 2, L, EPI, SPLIT>(p, grid, st); break;
+  }
+}
+
 template <typename T, int L, int EPI, bool SPLIT>
-void launch_main(const GemmParams<T>& p, dim3 grid, hipStream_t st) {
+void launch_main(int cfg, const GemmParams<T>& p, dim3 grid, hipStream_t st) {
   if constexpr (std::is_same<T, bf16_t>::value) {
-    hipLaunchKernelGGL((gemm_bf16_mfma<L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
+    launch_cfg<L, EPI, SPLIT>(cfg, p, grid, st);
   } else {
     hipLaunchKernelGGL((gemm_f32_fma<L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
   }
@@ -444,14 +702,12 @@ void launch_main(const GemmParams<T>& p, dim3 grid, hipStream_t st) {
 
 template <typename T, int L, int EPI>
 int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st) {
-  constexpr bool bf16 = std::is_same<T, bf16_t>::value;
   GemmParams<T> p = make_params<T>(d, pl, ws);
-  const int64_t bm = bf16 ? kBM : fBM, bn = bf16 ? kBN : fBN;
-  const int64_t tiles = rh_cdiv(d->M, bm) * rh_cdiv(d->N, bn);
+  const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
   if (tiles > INT32_MAX) return rh_set_error(RH_ERR_INVALID, "rh_gemm: too many tiles (%lld)", (long long)tiles);
   dim3 grid((unsigned)tiles, 1, (unsigned)pl.splits);
   if (pl.splits > 1) {
-    launch_main<T, L, EPI, true>(p, grid, st);
+    launch_main<T, L, EPI, true>(pl.cfg, p, grid, st);
     int rc = rh_check_launch("rh_gemm");
     if (rc) return rc;
     const int64_t total = d->M * d->N;
@@ -460,7 +716,7 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
     hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
     return rh_check_launch("rh_gemm split-k reduce");
   }
-  launch_main<T, L, EPI, false>(p, grid, st);
+  launch_main<T, L, EPI, false>(pl.cfg, p, grid, st);
   return rh_check_launch("rh_gemm");
 }
 
@@ -485,9 +741,8 @@ int launch_dtype(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st
 // Epilogue-only pass for K == 0 (acc = 0).
 template <typename T, int EPI>
 int launch_k0(const rh_gemm_desc* d, hipStream_t st) {
-  Plan pl{1, 0, 0};
+  Plan pl{kTf32, 1, 0, 0, 1, 1};
   GemmParams<T> p = make_params<T>(d, pl, nullptr);
-  // reuse the reduce kernel with zero splits: s = 0 for every element
   const int64_t total = d->M * d->N;
   int64_t blocks = rh_cdiv(total, 256);
   if (blocks > 4 * 1024) blocks = 4 * 1024;

@@ -41,10 +41,22 @@ def _gemm_ref(layout, A, B):
 SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8, 8), (513, 257, 1000)]
 
 
+@pytest.fixture(params=["auto", "0", "1", "2"])
+def gemm_tile(request, monkeypatch):
+    """Pin the bf16 GEMM tile shape (256x256 / 256x128 / 128x128) or let the planner choose."""
+    if request.param == "auto":
+        monkeypatch.delenv("RESIHP_GEMM_TILE", raising=False)
+    else:
+        monkeypatch.setenv("RESIHP_GEMM_TILE", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("layout", [H.RH_GEMM_NT, H.RH_GEMM_NN, H.RH_GEMM_TN])
 @pytest.mark.parametrize("M,N,K", SHAPES)
-def test_gemm_layouts(cuda, dtype, layout, M, N, K):
+def test_gemm_layouts(cuda, gemm_tile, dtype, layout, M, N, K):
+    if dtype == torch.float32 and gemm_tile != "auto":
+        pytest.skip("the tile override only applies to the bf16 kernels")
     a_shape = (K, M) if layout == H.RH_GEMM_TN else (M, K)
     b_shape = (N, K) if layout == H.RH_GEMM_NT else (K, N)
     A = _rand(*a_shape, dtype=dtype, seed=1)
@@ -55,20 +67,21 @@ def test_gemm_layouts(cuda, dtype, layout, M, N, K):
     assert err <= (BF16_TOL if dtype == torch.bfloat16 else F32_TOL), err
 
 
-@pytest.mark.parametrize("layout", [H.RH_GEMM_NN, H.RH_GEMM_TN])
-def test_gemm_split_k_matches_unsplit(cuda, layout):
+@pytest.mark.parametrize("layout", [H.RH_GEMM_NT, H.RH_GEMM_NN, H.RH_GEMM_TN])
+def test_gemm_split_k_matches_unsplit(cuda, gemm_tile, layout):
     """Few output tiles and a long K take the split-K path; it must agree with fp32."""
     M, N, K = 256, 384, 8192
     a_shape = (K, M) if layout == H.RH_GEMM_TN else (M, K)
+    b_shape = (N, K) if layout == H.RH_GEMM_NT else (K, N)
     A = _rand(*a_shape, seed=3)
-    B = _rand(K, N, seed=4)
+    B = _rand(*b_shape, seed=4)
     D = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
-    ops.gemm(layout, M, N, K, A, A.stride(0), [B], N, [D], N)
+    ops.gemm(layout, M, N, K, A, A.stride(0), [B], B.stride(0), [D], N)
     assert rel_inf(D, _gemm_ref(layout, A, B)) <= BF16_TOL
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gemm_epilogues(cuda, dtype):
+def test_gemm_epilogues(cuda, gemm_tile, dtype):
     M, N, K = 192, 320, 256
     A = _rand(M, K, dtype=dtype, seed=5)
     B = _rand(N, K, dtype=dtype, seed=6, scale=0.1)
@@ -96,7 +109,7 @@ def test_gemm_epilogues(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gemm_segments_act_as_one_matrix(cuda, dtype):
+def test_gemm_segments_act_as_one_matrix(cuda, gemm_tile, dtype):
     """Three separate q/k/v weights as B segments (forward, dgrad) and as D segments (wgrad)."""
     T, d, dl = 320, 256, 128
     tol = BF16_TOL if dtype == torch.bfloat16 else F32_TOL
@@ -310,3 +323,20 @@ def test_optimizer_steps(cuda, dtype):
     s.grad = grads[0].to(dtype)
     SGD([s], lr=1e-3).step()
     assert rel_inf(s, p0.to(dtype).float() - 1e-3 * grads[0].to(dtype).float()) <= (1e-7 if dtype == torch.float32 else 4e-3)
+
+
+def test_gemm_unaligned_views(cuda, gemm_tile):
+    """Operands and outputs that are column-offset views (rows not 16-byte aligned)."""
+    M, N, K = 300, 260, 200
+    Abuf = _rand(M, K + 3, seed=80)
+    Bbuf = _rand(N, K + 3, seed=81, scale=0.1)
+    Cbuf = _rand(M, N + 5, seed=82)
+    Dbuf = torch.zeros(M, N + 5, dtype=torch.bfloat16, device=cuda)
+    Ubuf = torch.zeros(M, N + 5, dtype=torch.bfloat16, device=cuda)
+    A, B, C, D, U = Abuf[:, 1:K + 1], Bbuf[:, 3:K + 3], Cbuf[:, 1:N + 1], Dbuf[:, 1:N + 1], Ubuf[:, 5:N + 5]
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, A.stride(0), [B], B.stride(0), [D], D.stride(0), beta=1.0, C=C,
+             ldc=C.stride(0), epilogue=H.RH_EPI_GELU, aux_out=U, ldaux=U.stride(0))
+    pre = A.float() @ B.float().t() + C.float()
+    assert rel_inf(U, pre) <= BF16_TOL
+    assert rel_inf(D, F.gelu(pre)) <= BF16_TOL
+    assert torch.all(Dbuf[:, 0] == 0) and torch.all(Ubuf[:, :5] == 0)  # nothing written outside the views
