@@ -57,7 +57,7 @@ struct AttnArgs {
 };
 
 // ---------------------------------------------------------------------------
-// delta_i = do_i . o_i   (fp32), one thread per (token, head)
+// delta_i = do_i . o_i   (fp32)
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void attn_delta(AttnArgs<T> a) {
@@ -72,6 +72,33 @@ __global__ __launch_bounds__(256) void attn_delta(AttnArgs<T> a) {
   for (int i = 0; i < a.D; ++i) s = fmaf(ld_f32(o + i), ld_f32(d + i), s);
   const int64_t b = t / a.S, sq = t % a.S;
   a.delta_out[(b * a.H + h) * a.S + sq] = s;
+}
+
+// bf16 rows with head_dim % 8 == 0 and 16-byte aligned rows: D/8 lanes per (token, head),
+// one 16-byte load of o and of do per lane, shuffle reduction over the D/8 lanes.
+template <int D>
+__global__ __launch_bounds__(256) void attn_delta_vec(AttnArgs<bf16_t> a) {
+  constexpr int L = D / 8;  // lanes per row (8 or 16)
+  const int64_t total = (int64_t)a.B * a.S * a.H;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / L;
+  const int part = threadIdx.x % L;
+  float s = 0.f;
+  int h = 0;
+  int64_t t = 0;
+  if (row < total) {
+    h = (int)(row % a.H);
+    t = row / a.H;
+    const u16x8_t o = *reinterpret_cast<const u16x8_t*>(a.o + t * a.ld_o + (int64_t)h * D + part * 8);
+    const u16x8_t d = *reinterpret_cast<const u16x8_t*>(a.dout + t * a.ld_do + (int64_t)h * D + part * 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = fmaf(bf16_to_f32(o[j]), bf16_to_f32(d[j]), s);
+  }
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (row < total && part == 0) {
+    const int64_t b = t / a.S, sq = t % a.S;
+    a.delta_out[(b * a.H + h) * a.S + sq] = s;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -284,17 +311,24 @@ __device__ __forceinline__ bf16x8_t pack8(const floatx16_t& v, int s) {
   return r;
 }
 
-// Gather a transposed operand fragment from a row-major LDS tile tile[row][col]:
-// element j = tile[r0 + j][col] for j < 4 and tile[r0 + 8 + (j-4)][col] for j >= 4.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// Transposed operand fragment from a row-major [token][P] LDS tile: rows of the MFMA operand are
+// 32 consecutive columns starting at c0, its eight k values are the tokens
+// r0 + {4g..4g+3, 8+4g..8+4g+3} (g = lane/32) -- the k order of accumulator registers
+// 8s..8s+7.  Two ds_read_b64_tr_b16: in each 16-lane block lane i addresses token row
+// (r0 + 4g + i/4 [+8]), columns c0 + 16*(block&1) + 4*(i%4) .. +3, and lane j receives
+// the four rows of column c0 + 16*(block&1) + j.
 template <int P>
-__device__ __forceinline__ bf16x8_t gather_t(const bf16_t (*tile)[P], int r0, int col) {
-  u16x8_t u;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    u[j] = tile[r0 + j][col];
-    u[4 + j] = tile[r0 + 8 + j][col];
-  }
-  return __builtin_bit_cast(bf16x8_t, u);
+__device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int c0, int lane) {
+  const int q = lane >> 4, i = lane & 15, g = q >> 1;
+  const int col = c0 + 16 * (q & 1) + 4 * (i & 3);
+  const int row = r0 + 4 * g + (i >> 2);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row * P + col));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + (row + 8) * P + col));
+  s16x4_t both[2] = {lo, hi};
+  return __builtin_bit_cast(bf16x8_t, both);
 }
 
 __device__ __forceinline__ bf16x8_t ld_frag(const bf16_t* p) {
@@ -309,24 +343,49 @@ __device__ __forceinline__ void st4(bf16_t* p, const floatx16_t& v, int rr, floa
   *reinterpret_cast<u16x4_t*>(p) = u;
 }
 
-// Copy `rows` rows of D bf16 each into an LDS tile (zero past `limit`).
-template <int D, int P>
-__device__ __forceinline__ void load_rows(bf16_t (*dst)[P], const bf16_t* base, int64_t ld, int r0, int rows,
-                                          int limit) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  for (int c = threadIdx.x; c < rows * CPR; c += 256) {
-    const int r = c / CPR, col = (c % CPR) * 8;
-    u16x8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (r0 + r < limit) v = *reinterpret_cast<const u16x8_t*>(base + (int64_t)(r0 + r) * ld + col);
-    *reinterpret_cast<u16x8_t*>(&dst[r][col]) = v;
+// ROWS x D bf16 rows staged global -> registers -> LDS (zero past `limit`), 256 threads.
+// `store` writes the row-major tile with pitch P1 and, when P2 > 0, a second copy with
+// pitch P2 (the copy read with transpose reads).
+template <int D, int ROWS>
+struct RowTile {
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int PER = ROWS * CPR / 256;      // chunks per thread
+  static_assert((ROWS * CPR) % 256 == 0, "tile must split evenly over 256 threads");
+  u16x8_t reg[PER];
+
+  __device__ __forceinline__ void load(const bf16_t* base, int64_t ld, int r0, int limit) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = threadIdx.x + i * 256, r = c / CPR, col = (c % CPR) * 8;
+      u16x8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (r0 + r < limit) v = *reinterpret_cast<const u16x8_t*>(base + (int64_t)(r0 + r) * ld + col);
+      reg[i] = v;
+    }
   }
-}
+  template <int P1, int P2>
+  __device__ __forceinline__ void store(bf16_t* s1, bf16_t* s2) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = threadIdx.x + i * 256, r = c / CPR, col = (c % CPR) * 8;
+      *reinterpret_cast<u16x8_t*>(s1 + r * P1 + col) = reg[i];
+      if (P2 > 0) *reinterpret_cast<u16x8_t*>(s2 + r * P2 + col) = reg[i];
+    }
+  }
+};
+
+// LDS pitches (elements): row reads with ds_read_b128 want 16 consecutive rows on distinct
+// 16-byte bank groups (pitch = D + 8); transpose reads touch 4 rows x 32 bytes per 16 lanes
+// and want rows 64 bytes apart modulo the 256-byte bank window (pitch = D + 32).
+template <int D> struct Pitch {
+  static constexpr int ROW = D + 8;
+  static constexpr int TR = D + 32;
+};
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_fwd_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BQ = 128, BKV = 64, KP = D + 8, KS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[BKV][KP];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[BKV][KP];
+  constexpr int BQ = 128, BKV = 64, KP = Pitch<D>::ROW, VP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
+  constexpr int STAGE = BKV * KP + BKV * VP;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int S = a.S, H = a.H;
   const int nqb = (S + BQ - 1) / BQ;
@@ -355,57 +414,74 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(AttnArgs<bf16_t> a) {
   const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
   const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
   const int kv_end = a.causal ? min(S, qb * BQ + BQ) : S;
-  for (int kt = 0; kt < kv_end; kt += BKV) {
-    __syncthreads();
-    load_rows<D, KP>(sK, kbase, a.ld_qkv, kt, BKV, S);
-    load_rows<D, KP>(sV, vbase, a.ld_qkv, kt, BKV, S);
-    __syncthreads();
-    if (wq0 >= S || (a.causal && kt > wq1)) continue;
-
-    floatx16_t st[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      st[kb] = zero16();
-#pragma unroll
-      for (int i = 0; i < KS; ++i) st[kb] = mfma32(ld_frag(&sK[kb * 32 + l32][16 * i + 8 * g]), qreg[i], st[kb]);
+  const int ntiles = (kv_end + BKV - 1) / BKV;
+  RowTile<D, BKV> tk, tv;
+  tk.load(kbase, a.ld_qkv, 0, S);
+  tv.load(vbase, a.ld_qkv, 0, S);
+  tk.template store<KP, 0>(smem, nullptr);
+  tv.template store<VP, 0>(smem + BKV * KP, nullptr);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int kt = t * BKV;
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      tk.load(kbase, a.ld_qkv, kt + BKV, S);
+      tv.load(vbase, a.ld_qkv, kt + BKV, S);
     }
-    float mx = -INFINITY;
+    const bf16_t* sK = smem + (t & 1) * STAGE;
+    const bf16_t* sV = sK + BKV * KP;
+    if (wq0 < S && !(a.causal && kt > wq1)) {
+      floatx16_t st[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        st[kb] = zero16();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        float s = st[kb][r] * c;
-        if (key >= S || (a.causal && key > q_row)) s = -INFINITY;
-        st[kb][r] = s;
-        mx = fmaxf(mx, s);
+        for (int i = 0; i < KS; ++i) st[kb] = mfma32(ld_frag(sK + (kb * 32 + l32) * KP + 16 * i + 8 * g), qreg[i], st[kb]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
-    const float corr = exp2f(m - mnew);
-    lsum *= corr;
+      float mx = -INFINITY;
+      const bool diag = a.causal && kt + BKV - 1 > wq0;  // some key in this tile is after some query
 #pragma unroll
-    for (int d = 0; d < DB; ++d)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          float sv = st[kb][r] * c;
+          if (key >= S || (diag && key > q_row)) sv = -INFINITY;
+          st[kb][r] = sv;
+          mx = fmaxf(mx, sv);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      const float corr = exp2f(m - mnew);
+      lsum *= corr;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int d = 0; d < DB; ++d)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(st[kb][r] - mnew);
-        st[kb][r] = p;
-        lsum += p;
-      }
-    m = mnew;
+        for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8_t pb = pack8(st[kb], s2);
-        const int r0 = kb * 32 + 16 * s2 + 4 * g;
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2f(st[kb][r] - mnew);
+          st[kb][r] = p;
+          lsum += p;
+        }
+      m = mnew;
 #pragma unroll
-        for (int d = 0; d < DB; ++d) oacc[d] = mfma32(gather_t<KP>(sV, r0, d * 32 + l32), pb, oacc[d]);
-      }
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8_t pb = pack8(st[kb], s2);
+#pragma unroll
+          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<VP>(sV, kb * 32 + 16 * s2, d * 32, lane), pb, oacc[d]);
+        }
+    }
+    if (more) {
+      bf16_t* nK = smem + ((t + 1) & 1) * STAGE;
+      tk.template store<KP, 0>(nK, nullptr);
+      tv.template store<VP, 0>(nK + BKV * KP, nullptr);
+    }
+    __syncthreads();
   }
   lsum += __shfl_xor(lsum, 32, 64);
   if (q_row >= S) return;
@@ -420,9 +496,9 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(AttnArgs<bf16_t> a) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BQ = 128, BKV = 64, KP = D + 8, KS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[BKV][KP];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[BKV][KP];
+  constexpr int BQ = 128, BKV = 64, KP = Pitch<D>::ROW, TP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
+  constexpr int STAGE = BKV * KP + BKV * TP + BKV * KP;  // K (row reads), K (transpose reads), V
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int S = a.S, H = a.H;
   const int nqb = (S + BQ - 1) / BQ;
@@ -457,35 +533,54 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a) {
   const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
   const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
   const int kv_end = a.causal ? min(S, qb * BQ + BQ) : S;
-  for (int kt = 0; kt < kv_end; kt += BKV) {
-    __syncthreads();
-    load_rows<D, KP>(sK, kbase, a.ld_qkv, kt, BKV, S);
-    load_rows<D, KP>(sV, vbase, a.ld_qkv, kt, BKV, S);
-    __syncthreads();
-    if (wq0 >= S || (a.causal && kt > wq1)) continue;
+  const int ntiles = (kv_end + BKV - 1) / BKV;
+  RowTile<D, BKV> tk, tv;
+  tk.load(kbase, a.ld_qkv, 0, S);
+  tv.load(vbase, a.ld_qkv, 0, S);
+  tk.template store<KP, TP>(smem, smem + BKV * KP);
+  tv.template store<KP, 0>(smem + BKV * KP + BKV * TP, nullptr);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int kt = t * BKV;
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      tk.load(kbase, a.ld_qkv, kt + BKV, S);
+      tv.load(vbase, a.ld_qkv, kt + BKV, S);
+    }
+    const bf16_t* sK = smem + (t & 1) * STAGE;
+    const bf16_t* sKt = sK + BKV * KP;
+    const bf16_t* sV = sKt + BKV * TP;
+    if (wq0 < S && !(a.causal && kt > wq1)) {
+      const bool diag = a.causal && kt + BKV - 1 > wq0;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      floatx16_t st = zero16(), dpt = zero16();
+      for (int kb = 0; kb < 2; ++kb) {
+        floatx16_t st = zero16(), dpt = zero16();
 #pragma unroll
-      for (int i = 0; i < KS; ++i) {
-        st = mfma32(ld_frag(&sK[kb * 32 + l32][16 * i + 8 * g]), qreg[i], st);
-        dpt = mfma32(ld_frag(&sV[kb * 32 + l32][16 * i + 8 * g]), doreg[i], dpt);
-      }
+        for (int i = 0; i < KS; ++i) {
+          st = mfma32(ld_frag(sK + (kb * 32 + l32) * KP + 16 * i + 8 * g), qreg[i], st);
+          dpt = mfma32(ld_frag(sV + (kb * 32 + l32) * KP + 16 * i + 8 * g), doreg[i], dpt);
+        }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const bool ok = key < S && q_row < S && !(a.causal && key > q_row);
-        const float p = ok ? exp2f(st[r] * c - lse2) : 0.f;
-        st[r] = p * (dpt[r] - del);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = key < S && q_row < S && !(diag && key > q_row);
+          const float p = ok ? exp2f(st[r] * c - lse2) : 0.f;
+          st[r] = p * (dpt[r] - del);
+        }
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8_t dsb = pack8(st, s2);
-        const int r0 = kb * 32 + 16 * s2 + 4 * g;
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8_t dsb = pack8(st, s2);
 #pragma unroll
-        for (int d = 0; d < DB; ++d) dqt[d] = mfma32(gather_t<KP>(sK, r0, d * 32 + l32), dsb, dqt[d]);
+          for (int d = 0; d < DB; ++d) dqt[d] = mfma32(tr_frag<TP>(sKt, kb * 32 + 16 * s2, d * 32, lane), dsb, dqt[d]);
+        }
       }
     }
+    if (more) {
+      bf16_t* nK = smem + ((t + 1) & 1) * STAGE;
+      tk.template store<KP, TP>(nK, nK + BKV * KP);
+      tv.template store<KP, 0>(nK + BKV * KP + BKV * TP, nullptr);
+    }
+    __syncthreads();
   }
   if (q_row >= S) return;
   bf16_t* dqp = a.dq + (tok0 + q_row) * a.ld_d + (int64_t)h * D;
@@ -497,10 +592,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BK = 128, BQT = 32, KP = D + 8, KS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[BQT][KP];
-  __shared__ __attribute__((aligned(16))) bf16_t sdO[BQT][KP];
-  __shared__ float sL[BQT], sDel[BQT];
+  constexpr int BK = 128, BQT = 32, RP = Pitch<D>::ROW, TP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
+  constexpr int STAGE = 2 * BQT * RP + 2 * BQT * TP;  // Q, dO (row reads); Q, dO (transpose reads)
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
+  __shared__ float sL[2][BQT], sDel[2][BQT];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int S = a.S, H = a.H;
   const int kblk = blockIdx.x;  // block 0 has the most causal work; launched first
@@ -534,42 +629,70 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a) {
   const bf16_t* qbase = a.q + tok0 * a.ld_qkv + (int64_t)h * D;
   const bf16_t* dbase = a.dout + tok0 * a.ld_do + (int64_t)h * D;
   const int q_start = a.causal ? kblk * BK : 0;
-  for (int qt = q_start; qt < S; qt += BQT) {
-    __syncthreads();
-    load_rows<D, KP>(sQ, qbase, a.ld_qkv, qt, BQT, S);
-    load_rows<D, KP>(sdO, dbase, a.ld_do, qt, BQT, S);
+  const int ntiles = q_start < S ? (S - q_start + BQT - 1) / BQT : 0;
+  RowTile<D, BQT> tq, td;
+  float l_pref = 0.f, d_pref = 0.f;
+  auto load_tile = [&](int qt) {
+    tq.load(qbase, a.ld_qkv, qt, S);
+    td.load(dbase, a.ld_do, qt, S);
     if (tid < BQT) {
       const int q = qt + tid;
-      sL[tid] = q < S ? a.lse[(int64_t)bh * S + q] * kLog2e : 0.f;
-      sDel[tid] = q < S ? a.delta[(int64_t)bh * S + q] : 0.f;
+      l_pref = q < S ? a.lse[(int64_t)bh * S + q] * kLog2e : 0.f;
+      d_pref = q < S ? a.delta[(int64_t)bh * S + q] : 0.f;
     }
-    __syncthreads();
-    if (wk0 >= S || (a.causal && qt + BQT - 1 < wk0)) continue;
-    floatx16_t s = zero16(), dp = zero16();
-#pragma unroll
-    for (int i = 0; i < KS; ++i) {
-      s = mfma32(ld_frag(&sQ[l32][16 * i + 8 * g]), kreg[i], s);
-      dp = mfma32(ld_frag(&sdO[l32][16 * i + 8 * g]), vreg[i], dp);
+  };
+  auto store_tile = [&](int stage) {
+    bf16_t* base = smem + stage * STAGE;
+    tq.template store<RP, TP>(base, base + 2 * BQT * RP);
+    td.template store<RP, TP>(base + BQT * RP, base + 2 * BQT * RP + BQT * TP);
+    if (tid < BQT) {
+      sL[stage][tid] = l_pref;
+      sDel[stage][tid] = d_pref;
     }
+  };
+  if (ntiles > 0) {
+    load_tile(q_start);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int qt = q_start + t * BQT;
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(qt + BQT);
+    const int cur = t & 1;
+    const bf16_t* sQ = smem + cur * STAGE;
+    const bf16_t* sdO = sQ + BQT * RP;
+    const bf16_t* sQt = sQ + 2 * BQT * RP;
+    const bf16_t* sdOt = sQt + BQT * TP;
+    if (wk0 < S && !(a.causal && qt + BQT - 1 < wk0)) {
+      floatx16_t sc = zero16(), dp = zero16();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qi = 8 * (r >> 2) + 4 * g + (r & 3);
-      const int q = qt + qi;
-      const bool ok = q < S && key < S && !(a.causal && key > q);
-      const float p = ok ? exp2f(s[r] * c - sL[qi]) : 0.f;
-      dp[r] = p * (dp[r] - sDel[qi]);
-      s[r] = p;
-    }
+      for (int i = 0; i < KS; ++i) {
+        sc = mfma32(ld_frag(sQ + l32 * RP + 16 * i + 8 * g), kreg[i], sc);
+        dp = mfma32(ld_frag(sdO + l32 * RP + 16 * i + 8 * g), vreg[i], dp);
+      }
+      const bool diag = a.causal && qt < wk0 + 31;  // some query in this tile precedes some key
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const bf16x8_t pb = pack8(s, s2), dsb = pack8(dp, s2);
-      const int r0 = 16 * s2 + 4 * g;
+      for (int r = 0; r < 16; ++r) {
+        const int qi = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int q = qt + qi;
+        const bool ok = q < S && key < S && !(diag && key > q);
+        const float p = ok ? exp2f(sc[r] * c - sL[cur][qi]) : 0.f;
+        dp[r] = p * (dp[r] - sDel[cur][qi]);
+        sc[r] = p;
+      }
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        dvt[d] = mfma32(gather_t<KP>(sdO, r0, d * 32 + l32), pb, dvt[d]);
-        dkt[d] = mfma32(gather_t<KP>(sQ, r0, d * 32 + l32), dsb, dkt[d]);
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const bf16x8_t pb = pack8(sc, s2), dsb = pack8(dp, s2);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          dvt[d] = mfma32(tr_frag<TP>(sdOt, 16 * s2, d * 32, lane), pb, dvt[d]);
+          dkt[d] = mfma32(tr_frag<TP>(sQt, 16 * s2, d * 32, lane), dsb, dkt[d]);
+        }
       }
     }
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
   }
   if (key >= S) return;
   bf16_t* dkp = a.dk + (tok0 + key) * a.ld_d + (int64_t)h * D;
@@ -697,7 +820,13 @@ extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
     a.o = (const bf16_t*)o; a.ld_o = ld_o; a.dout = (const bf16_t*)dout; a.ld_do = ld_do;
     a.lse = lse; a.delta = delta; a.delta_out = delta;
     a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv; a.ld_d = ld_dqkv;
-    hipLaunchKernelGGL(attn_delta<bf16_t>, dim3(dblocks), dim3(256), 0, st, a);
+    if (mfma_ok(dtype, head_dim, {o, dout}, {ld_o, ld_do})) {
+      const unsigned vblocks = (unsigned)((rows * (head_dim / 8) + 255) / 256);
+      if (head_dim == 64) hipLaunchKernelGGL(attn_delta_vec<64>, dim3(vblocks), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL(attn_delta_vec<128>, dim3(vblocks), dim3(256), 0, st, a);
+    } else {
+      hipLaunchKernelGGL(attn_delta<bf16_t>, dim3(dblocks), dim3(256), 0, st, a);
+    }
     if (mfma_ok(dtype, head_dim, {q, k, v, dout, dq, dk, dv}, {ld_qkv, ld_do, ld_dqkv})) {
       dim3 gq((unsigned)((seq + 127) / 128), (unsigned)(batch * heads));
       dim3 gk((unsigned)((seq + 127) / 128), (unsigned)(batch * heads));

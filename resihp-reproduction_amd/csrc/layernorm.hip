@@ -196,23 +196,37 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(int64_t rows, int dim, cons
   }
 }
 
+// Column sums of the per-block partial rows: a block owns 64 columns; wave w sums partial
+// rows w, w+4, ... for its lane's column, and the four wave sums are added in wave order
+// (fixed order: deterministic).
 template <typename T>
 __global__ __launch_bounds__(256) void ln_colsum_kernel(int nblocks, int dim, const float* __restrict__ part_g,
                                                          const float* __restrict__ part_b, T* dgamma, T* dbeta,
                                                          int accumulate) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= dim) return;
+  __shared__ float red[2][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
   float sg = 0.f, sb = 0.f;
-  for (int b = 0; b < nblocks; ++b) {
-    sg += part_g[(int64_t)b * dim + col];
-    sb += part_b[(int64_t)b * dim + col];
+  if (col < dim) {
+#pragma unroll 8
+    for (int b = wave; b < nblocks; b += 4) {
+      sg += part_g[(int64_t)b * dim + col];
+      sb += part_b[(int64_t)b * dim + col];
+    }
   }
-  if (dgamma) st_f32(dgamma + col, accumulate ? ld_f32(dgamma + col) + sg : sg);
-  if (dbeta) st_f32(dbeta + col, accumulate ? ld_f32(dbeta + col) + sb : sb);
+  red[0][wave][lane] = sg;
+  red[1][wave][lane] = sb;
+  __syncthreads();
+  if (wave == 0 && col < dim) {
+    sg = red[0][0][lane] + red[0][1][lane] + red[0][2][lane] + red[0][3][lane];
+    sb = red[1][0][lane] + red[1][1][lane] + red[1][2][lane] + red[1][3][lane];
+    if (dgamma) st_f32(dgamma + col, accumulate ? ld_f32(dgamma + col) + sg : sg);
+    if (dbeta) st_f32(dbeta + col, accumulate ? ld_f32(dbeta + col) + sb : sb);
+  }
 }
 
 int ln_blocks(int64_t rows) {
-  int64_t nb = rh_cdiv(rows, 32);
+  int64_t nb = rh_cdiv(rows, 16);
   if (nb > 512) nb = 512;
   if (nb < 1) nb = 1;
   return (int)nb;
@@ -323,7 +337,7 @@ extern "C" int rh_layernorm_bwd(int dtype, int64_t rows, int64_t dim, const void
                                          pb, nb, st);
   if (rc) return rc;
   if (dgamma || dbeta) {
-    const unsigned blocks = (unsigned)rh_cdiv(dim, 256);
+    const unsigned blocks = (unsigned)rh_cdiv(dim, 64);
     if (dtype == RH_DTYPE_BF16)
       hipLaunchKernelGGL(ln_colsum_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, nb, (int)dim, pg, pb,
                          (bf16_t*)dgamma, (bf16_t*)dbeta, accumulate);
