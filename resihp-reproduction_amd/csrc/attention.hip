@@ -9,18 +9,19 @@
 // P is rebuilt from lse in the backward; the [S,S] matrix never reaches HBM.
 //
 // bf16 / head_dim 64 or 128: MFMA kernels built on v_mfma_f32_32x32x16_bf16.
-// Scores are computed transposed (S^T = K Q^T) so that every lane owns ONE
-// query (its column) and 16 keys per 32-key block: the row max / row sum of
-// the online softmax are lane-local plus one exchange with lane^32, and the
-// probabilities feed the next MFMA (O^T += V^T P^T) straight from registers.
+// Scores are computed transposed (S^T = K Q^T, or S = Q K^T in the dK/dV kernel) so that
+// every lane owns ONE query (one key) and 16 rows of each 32-row block: row max / row sum
+// of the online softmax are lane-local plus one exchange with lane^32, and the
+// probabilities feed the next MFMA straight from registers.
 // 32x32 accumulator layout used throughout: register r of lane l holds
 //   row 8*(r/4) + 4*(l/32) + r%4, column l%32;
 // an operand fragment of lane l holds row/column l%32 and eight k values.
-// The eight k values of lane group g = l/32 at step s of a 32-key block are the
-// keys 16s + {4g..4g+3, 8+4g..8+4g+3}: exactly accumulator registers 8s..8s+7
-// of the score tile, so P^T needs no data movement.  The matching V^T / Q^T /
-// dO^T / K^T fragments are gathered from row-major LDS tiles.
-//
+// The eight k values of lane group g = l/32 at step s of a 32-row block are the rows
+// 16s + {4g..4g+3, 8+4g..8+4g+3}: exactly accumulator registers 8s..8s+7 of the score
+// tile, so P^T needs no data movement; the matching V^T / K^T / dO^T / Q^T fragments
+// are read from the same swizzled LDS tiles with ds_read_b64_tr_b16.
+// Backward runs dQ first (it also produces delta) and then dK/dV; neither uses atomics,
+// so results are bit-reproducible.
 // Everything else (fp32, other head sizes): one thread per query (forward, dq)
 // or per key (dk/dv) with K/V or Q/dO tiles staged in LDS; fp32 FMA.
 #include <initializer_list>
@@ -72,33 +73,6 @@ __global__ __launch_bounds__(256) void attn_delta(AttnArgs<T> a) {
   for (int i = 0; i < a.D; ++i) s = fmaf(ld_f32(o + i), ld_f32(d + i), s);
   const int64_t b = t / a.S, sq = t % a.S;
   a.delta_out[(b * a.H + h) * a.S + sq] = s;
-}
-
-// bf16 rows with head_dim % 8 == 0 and 16-byte aligned rows: D/8 lanes per (token, head),
-// one 16-byte load of o and of do per lane, shuffle reduction over the D/8 lanes.
-template <int D>
-__global__ __launch_bounds__(256) void attn_delta_vec(AttnArgs<bf16_t> a) {
-  constexpr int L = D / 8;  // lanes per row (8 or 16)
-  const int64_t total = (int64_t)a.B * a.S * a.H;
-  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / L;
-  const int part = threadIdx.x % L;
-  float s = 0.f;
-  int h = 0;
-  int64_t t = 0;
-  if (row < total) {
-    h = (int)(row % a.H);
-    t = row / a.H;
-    const u16x8_t o = *reinterpret_cast<const u16x8_t*>(a.o + t * a.ld_o + (int64_t)h * D + part * 8);
-    const u16x8_t d = *reinterpret_cast<const u16x8_t*>(a.dout + t * a.ld_do + (int64_t)h * D + part * 8);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s = fmaf(bf16_to_f32(o[j]), bf16_to_f32(d[j]), s);
-  }
-#pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (row < total && part == 0) {
-    const int64_t b = t / a.S, sq = t % a.S;
-    a.delta_out[(b * a.H + h) * a.S + sq] = s;
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -292,6 +266,14 @@ __global__ __launch_bounds__(gQ) void attn_bwd_dkdv_generic(AttnArgs<T> a) {
 // ---------------------------------------------------------------------------
 // MFMA kernels (bf16, head_dim D in {64, 128})
 // ---------------------------------------------------------------------------
+// Work decomposition (all three kernels): an item is one (batch*head, 64-row block) pair --
+// 64 queries for the forward and dQ kernels, 64 keys for the dK/dV kernel.  Items are
+// numbered longest-causal-work first and workgroup c runs items c and n-1-c, so every
+// workgroup gets the same amount of causal work.  A workgroup has 8 waves (two per SIMD):
+// wave w owns 32 rows of the item (w & 1) and one of 4 phases (w >> 1).  Each stage streams
+// 128 rows of the other operand (keys, or queries for dK/dV) into LDS; phase p works on
+// rows 32p..32p+31 of the stage, and the 4 phases' partial results are merged in LDS at the
+// end of the item in phase order (deterministic).
 __device__ __forceinline__ floatx16_t mfma32(bf16x8_t a, bf16x8_t b, floatx16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -313,27 +295,66 @@ __device__ __forceinline__ bf16x8_t pack8(const floatx16_t& v, int s) {
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Transposed operand fragment from a row-major [token][P] LDS tile: rows of the MFMA operand are
-// 32 consecutive columns starting at c0, its eight k values are the tokens
-// r0 + {4g..4g+3, 8+4g..8+4g+3} (g = lane/32) -- the k order of accumulator registers
-// 8s..8s+7.  Two ds_read_b64_tr_b16: in each 16-lane block lane i addresses token row
-// (r0 + 4g + i/4 [+8]), columns c0 + 16*(block&1) + 4*(i%4) .. +3, and lane j receives
-// the four rows of column c0 + 16*(block&1) + j.
-template <int P>
+// Element offset of (row r, column c) in a swizzled [rows][D] bf16 LDS tile.  The 16-byte
+// chunk c/8 of row r is stored at chunk (c/8) ^ sw(r).  sw is chosen so that
+//   * a ds_read_b128 of 16 consecutive rows at one chunk touches 16 distinct bank groups;
+//   * a ds_read_b64_tr_b16 half-wave (4 consecutive rows x 2 adjacent 32-byte column pieces)
+//     touches 8 distinct 32-byte bank groups.
+template <int D>
+__device__ __forceinline__ int swz(int r, int c) {
+  const int sw = D == 128 ? (4 * (r & 3) + ((r >> 2) & 3)) : (4 * ((r >> 1) & 1) + ((r >> 2) & 3));
+  return r * D + ((((c >> 3) ^ sw)) << 3) + (c & 7);
+}
+
+// Operand fragment of rows r0 + lane%32, eight columns c0 + 8*(lane/32).. (ds_read_b128).
+template <int D>
+__device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int c0, int lane) {
+  return *reinterpret_cast<const bf16x8_t*>(tile + swz<D>(r0 + (lane & 31), c0 + 8 * (lane >> 5)));
+}
+
+// Transposed operand fragment: rows of the MFMA operand are the 32 tile columns c0..c0+31,
+// its eight k values are the tile rows r0 + {4g..4g+3, 8+4g..8+4g+3} (g = lane/32) -- the k
+// order of accumulator registers 8s..8s+7.  Two ds_read_b64_tr_b16: in each 16-lane block,
+// lane i addresses tile row r0 + 4g + i/4 (+8), columns c0 + 16*(block&1) + 4*(i%4)..+3, and
+// lane j receives those four rows of column c0 + 16*(block&1) + j.
+template <int D>
 __device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int c0, int lane) {
   const int q = lane >> 4, i = lane & 15, g = q >> 1;
   const int col = c0 + 16 * (q & 1) + 4 * (i & 3);
   const int row = r0 + 4 * g + (i >> 2);
-  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row * P + col));
-  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + (row + 8) * P + col));
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + swz<D>(row, col)));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + swz<D>(row + 8, col)));
   s16x4_t both[2] = {lo, hi};
   return __builtin_bit_cast(bf16x8_t, both);
 }
 
-__device__ __forceinline__ bf16x8_t ld_frag(const bf16_t* p) {
-  return *reinterpret_cast<const bf16x8_t*>(p);
+// ROWS rows x D of a [token][ld] bf16 matrix (rows r0.., clamped to `last`) into a swizzled
+// LDS tile with direct global->LDS loads.  Each wave fills whole 1 KB windows of the tile: lane
+// l of a window lands at window byte 16*l, i.e. physical chunk l % (D/8) of row
+// l / (D/8); it therefore fetches the logical chunk that the swizzle puts there.  Rows past
+// `last` repeat row `last`: every consumer masks them out of the result.
+template <int D, int ROWS = 128>
+__device__ __forceinline__ void dma_rows(bf16_t* tile, const bf16_t* base, int64_t ld, int r0, int last, int wave,
+                                         int lane) {
+  constexpr int CPR = D / 8;                // 16-byte chunks per row
+  constexpr int RPW = 64 / CPR;             // rows per 1 KB window
+  constexpr int WINDOWS = ROWS / RPW;       // windows per tile
+  static_assert(WINDOWS % 8 == 0, "tile windows must split evenly over 8 waves");
+#pragma unroll
+  for (int i = 0; i < WINDOWS / 8; ++i) {
+    const int win = wave + 8 * i;
+    const int row = win * RPW + lane / CPR;
+    const int pchunk = lane % CPR;
+    const int sw = D == 128 ? (4 * (row & 3) + ((row >> 2) & 3)) : (4 * ((row >> 1) & 1) + ((row >> 2) & 3));
+    const int grow = min(r0 + row, last);
+    const bf16_t* src = base + (int64_t)grow * ld + ((pchunk ^ sw) << 3);
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(tile + win * 512), 16, 0, 0);
+  }
 }
+
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Store 4 consecutive head-dim values (registers 4rr..4rr+3) as bf16.
 __device__ __forceinline__ void st4(bf16_t* p, const floatx16_t& v, int rr, float mul) {
@@ -343,367 +364,416 @@ __device__ __forceinline__ void st4(bf16_t* p, const floatx16_t& v, int rr, floa
   *reinterpret_cast<u16x4_t*>(p) = u;
 }
 
-// ROWS x D bf16 rows staged global -> registers -> LDS (zero past `limit`), 256 threads.
-// `store` writes the row-major tile with pitch P1 and, when P2 > 0, a second copy with
-// pitch P2 (the copy read with transpose reads).
-template <int D, int ROWS>
-struct RowTile {
-  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int PER = ROWS * CPR / 256;      // chunks per thread
-  static_assert((ROWS * CPR) % 256 == 0, "tile must split evenly over 256 threads");
-  u16x8_t reg[PER];
+// Load the 8 k-slices (16 d each) of one head-row as MFMA operand registers: lane l holds
+// d = 16i + 8*(l/32) .. +7 of row `row` for slice i.
+template <int KS>
+__device__ __forceinline__ void load_head_row(bf16x8_t (&r)[KS], const bf16_t* p, bool ok, int g) {
+#pragma unroll
+  for (int i = 0; i < KS; ++i) {
+    u16x8_t u = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (ok) u = *reinterpret_cast<const u16x8_t*>(p + 16 * i + 8 * g);
+    r[i] = __builtin_bit_cast(bf16x8_t, u);
+  }
+}
 
-  __device__ __forceinline__ void load(const bf16_t* base, int64_t ld, int r0, int limit) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = threadIdx.x + i * 256, r = c / CPR, col = (c % CPR) * 8;
-      u16x8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (r0 + r < limit) v = *reinterpret_cast<const u16x8_t*>(base + (int64_t)(r0 + r) * ld + col);
-      reg[i] = v;
-    }
-  }
-  template <int P1, int P2>
-  __device__ __forceinline__ void store(bf16_t* s1, bf16_t* s2) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = threadIdx.x + i * 256, r = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<u16x8_t*>(s1 + r * P1 + col) = reg[i];
-      if (P2 > 0) *reinterpret_cast<u16x8_t*>(s2 + r * P2 + col) = reg[i];
-    }
-  }
+// item -> (batch*head, block), longest causal work first
+struct Item {
+  int bh, blk;
 };
+__device__ __forceinline__ Item item_q(int item, int BH, int nblk) { return {item % BH, nblk - 1 - item / BH}; }
+__device__ __forceinline__ Item item_k(int item, int BH) { return {item % BH, item / BH}; }
 
-// LDS pitches (elements): row reads with ds_read_b128 want 16 consecutive rows on distinct
-// 16-byte bank groups (pitch = D + 8); transpose reads touch 4 rows x 32 bytes per 16 lanes
-// and want rows 64 bytes apart modulo the 256-byte bank window (pitch = D + 32).
-template <int D> struct Pitch {
-  static constexpr int ROW = D + 8;
-  static constexpr int TR = D + 32;
-};
+constexpr int kPhases = 4, kStageRows = 128;
 
-template <int D>
-__global__ __launch_bounds__(256) void attn_fwd_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BQ = 128, BKV = 64, KP = Pitch<D>::ROW, VP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
-  constexpr int STAGE = BKV * KP + BKV * VP;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int S = a.S, H = a.H;
-  const int nqb = (S + BQ - 1) / BQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int64_t tok0 = (int64_t)b * S;
-  const int wq0 = qb * BQ + w * 32, wq1 = wq0 + 31;
-  const int q_row = wq0 + l32;
-  const float c = a.scale * kLog2e;
-
-  bf16x8_t qreg[KS];
-  {
-    const bf16_t* qp = a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D;
+// Merge per-phase fp32 register tiles (acc[OFF..OFF+NACC) per lane) of the 6 waves with phase > 0
+// into the phase-0 waves, in phase order.  `cbuf` needs 6 * NACC * 16 * 64 floats.  On return
+// (phase-0 waves) acc holds the sum.  Ends with the LDS free for reuse.
+template <int OFF, int NACC, int N>
+__device__ __forceinline__ void merge_phases(float* cbuf, floatx16_t (&acc)[N], int wave, int lane) {
+  static_assert(OFF + NACC <= N, "merge range outside the accumulator array");
+  const int sub = wave & 1, ph = wave >> 1;
+  if (ph > 0) {
+    float* dst = cbuf + (size_t)((ph - 1) * 2 + sub) * NACC * 16 * 64;
 #pragma unroll
-    for (int i = 0; i < KS; ++i) {
-      u16x8_t u = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (q_row < S) u = *reinterpret_cast<const u16x8_t*>(qp + 16 * i + 8 * g);
-      qreg[i] = __builtin_bit_cast(bf16x8_t, u);
-    }
+    for (int d = 0; d < NACC; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[(d * 16 + r) * 64 + lane] = acc[OFF + d][r];
   }
-  floatx16_t oacc[DB];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) oacc[d] = zero16();
-  float m = -INFINITY, lsum = 0.f;
-
-  const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
-  const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
-  const int kv_end = a.causal ? min(S, qb * BQ + BQ) : S;
-  const int ntiles = (kv_end + BKV - 1) / BKV;
-  RowTile<D, BKV> tk, tv;
-  tk.load(kbase, a.ld_qkv, 0, S);
-  tv.load(vbase, a.ld_qkv, 0, S);
-  tk.template store<KP, 0>(smem, nullptr);
-  tv.template store<VP, 0>(smem + BKV * KP, nullptr);
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int kt = t * BKV;
-    const bool more = t + 1 < ntiles;
-    if (more) {
-      tk.load(kbase, a.ld_qkv, kt + BKV, S);
-      tv.load(vbase, a.ld_qkv, kt + BKV, S);
+  if (ph == 0) {
+#pragma unroll 1
+    for (int p = 1; p < kPhases; ++p) {
+      const float* src = cbuf + (size_t)((p - 1) * 2 + sub) * NACC * 16 * 64;
+#pragma unroll
+      for (int d = 0; d < NACC; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[OFF + d][r] += src[(d * 16 + r) * 64 + lane];
     }
-    const bf16_t* sK = smem + (t & 1) * STAGE;
-    const bf16_t* sV = sK + BKV * KP;
-    if (wq0 < S && !(a.causal && kt > wq1)) {
-      floatx16_t st[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        st[kb] = zero16();
-#pragma unroll
-        for (int i = 0; i < KS; ++i) st[kb] = mfma32(ld_frag(sK + (kb * 32 + l32) * KP + 16 * i + 8 * g), qreg[i], st[kb]);
-      }
-      float mx = -INFINITY;
-      const bool diag = a.causal && kt + BKV - 1 > wq0;  // some key in this tile is after some query
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          float sv = st[kb][r] * c;
-          if (key >= S || (diag && key > q_row)) sv = -INFINITY;
-          st[kb][r] = sv;
-          mx = fmaxf(mx, sv);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx);
-      const float corr = exp2f(m - mnew);
-      lsum *= corr;
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(st[kb][r] - mnew);
-          st[kb][r] = p;
-          lsum += p;
-        }
-      m = mnew;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8_t pb = pack8(st[kb], s2);
-#pragma unroll
-          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<VP>(sV, kb * 32 + 16 * s2, d * 32, lane), pb, oacc[d]);
-        }
-    }
-    if (more) {
-      bf16_t* nK = smem + ((t + 1) & 1) * STAGE;
-      tk.template store<KP, 0>(nK, nullptr);
-      tv.template store<VP, 0>(nK + BKV * KP, nullptr);
-    }
-    __syncthreads();
   }
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (q_row >= S) return;
-  const float inv = 1.f / lsum;
-  bf16_t* op = a.o_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
-#pragma unroll
-  for (int d = 0; d < DB; ++d)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) st4(op + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
-  if (g == 0) a.lse_out[(int64_t)bh * S + q_row] = (m + log2f(lsum)) * kLn2;
+  __syncthreads();
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BQ = 128, BKV = 64, KP = Pitch<D>::ROW, TP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
-  constexpr int STAGE = BKV * KP + BKV * TP + BKV * KP;  // K (row reads), K (transpose reads), V
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
+__global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nitems) {
+  constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
+  static_assert((6 * DB * 16 * 64 + 1024) * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int S = a.S, H = a.H;
-  const int nqb = (S + BQ - 1) / BQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int64_t tok0 = (int64_t)b * S;
-  const int wq0 = qb * BQ + w * 32, wq1 = wq0 + 31;
-  const int q_row = wq0 + l32;
+  const int sub = w & 1, ph = w >> 1;
+  const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
+  float* cbuf = reinterpret_cast<float*>(smem);
 
-  bf16x8_t qreg[KS], doreg[KS];
-  {
-    const bf16_t* qp = a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D;
-    const bf16_t* dp = a.dout + (tok0 + q_row) * a.ld_do + (int64_t)h * D;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
+    if (pass == 1 && item <= (int)blockIdx.x) break;
+    const Item it = item_q(item, BH, nqb);
+    const int b = it.bh / H, h = it.bh % H;
+    const int64_t tok0 = (int64_t)b * S;
+    const int wq0 = it.blk * 64 + 32 * sub, wq1 = wq0 + 31, q_row = wq0 + l32;
+
+    bf16x8_t qreg[KS];
+    load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, q_row < S, g);
+    floatx16_t oacc[DB];
 #pragma unroll
-    for (int i = 0; i < KS; ++i) {
-      u16x8_t u = {0, 0, 0, 0, 0, 0, 0, 0}, v = u;
-      if (q_row < S) {
-        u = *reinterpret_cast<const u16x8_t*>(qp + 16 * i + 8 * g);
-        v = *reinterpret_cast<const u16x8_t*>(dp + 16 * i + 8 * g);
+    for (int d = 0; d < DB; ++d) oacc[d] = zero16();
+    float m = -INFINITY, lsum = 0.f;
+
+    const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
+    const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
+    const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
+    const int nst = (kv_end + kStageRows - 1) / kStageRows;
+    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
+    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
+    wait_vm();
+    __syncthreads();
+    for (int t = 0; t < nst; ++t) {
+      if (t + 1 < nst) {
+        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+        dma_rows<D>(nxt, kbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
+        dma_rows<D>(nxt + TILE, vbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
       }
-      qreg[i] = __builtin_bit_cast(bf16x8_t, u);
-      doreg[i] = __builtin_bit_cast(bf16x8_t, v);
+      const bf16_t* sK = smem + (t & 1) * 2 * TILE;
+      const bf16_t* sV = sK + TILE;
+      const int kt0 = t * kStageRows + 32 * ph;
+      if (wq0 < S && kt0 < kv_end && !(a.causal && kt0 > wq1)) {
+        floatx16_t st = zero16();
+#pragma unroll
+        for (int i = 0; i < KS; ++i) st = mfma32(row_frag<D>(sK, 32 * ph, 16 * i, lane), qreg[i], st);
+        const bool diag = a.causal && kt0 + 31 > wq0;
+        const bool tail = kt0 + 31 >= S;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
+          float sv = st[r] * c;
+          if ((tail && key >= S) || (diag && key > q_row)) sv = -INFINITY;
+          st[r] = sv;
+          mx = fmaxf(mx, sv);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float corr = __builtin_amdgcn_exp2f(m - mnew);
+        lsum *= corr;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(st[r] - mnew);
+          st[r] = p;
+          lsum += p;
+        }
+        m = mnew;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8_t pb = pack8(st, s2);
+#pragma unroll
+          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<D>(sV, 32 * ph + 16 * s2, d * 32, lane), pb, oacc[d]);
+        }
+      }
+      wait_vm();
+      __syncthreads();
+    }
+    // merge the 4 phases: rescale each phase's partial to the common max, then sum in order
+    float* mbuf = cbuf + 6 * DB * 16 * 64;  // m and lsum of every wave, [phase][sub][lane]
+    mbuf[(ph * 2 + sub) * 64 + lane] = m;
+    mbuf[512 + (ph * 2 + sub) * 64 + lane] = lsum;
+    __syncthreads();
+    float mall = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < kPhases; ++p) mall = fmaxf(mall, mbuf[(p * 2 + sub) * 64 + lane]);
+    const float own = m == -INFINITY ? 0.f : exp2f(m - mall);
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[d][r] *= own;
+    float lall = 0.f;
+    if (ph == 0) {
+#pragma unroll
+      for (int p = 0; p < kPhases; ++p) {
+        const float mp = mbuf[(p * 2 + sub) * 64 + lane];
+        const float f = mp == -INFINITY ? 0.f : exp2f(mp - mall);
+        lall += f * mbuf[512 + (p * 2 + sub) * 64 + lane];
+      }
+    }
+    merge_phases<0, DB>(cbuf, oacc, w, lane);
+    if (ph == 0) {
+      lall += __shfl_xor(lall, 32, 64);
+      if (q_row < S) {
+        const float inv = 1.f / lall;
+        bf16_t* op = a.o_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) st4(op + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
+        if (g == 0) a.lse_out[(int64_t)it.bh * S + q_row] = (mall + log2f(lall)) * kLn2;
+      }
     }
   }
-  const float lse2 = q_row < S ? a.lse[(int64_t)bh * S + q_row] * kLog2e : 0.f;
-  const float del = q_row < S ? a.delta[(int64_t)bh * S + q_row] : 0.f;
-  floatx16_t dqt[DB];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) dqt[d] = zero16();
+}
 
-  const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
-  const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
-  const int kv_end = a.causal ? min(S, qb * BQ + BQ) : S;
-  const int ntiles = (kv_end + BKV - 1) / BKV;
-  RowTile<D, BKV> tk, tv;
-  tk.load(kbase, a.ld_qkv, 0, S);
-  tv.load(vbase, a.ld_qkv, 0, S);
-  tk.template store<KP, TP>(smem, smem + BKV * KP);
-  tv.template store<KP, 0>(smem + BKV * KP + BKV * TP, nullptr);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int kt = t * BKV;
-    const bool more = t + 1 < ntiles;
-    if (more) {
-      tk.load(kbase, a.ld_qkv, kt + BKV, S);
-      tv.load(vbase, a.ld_qkv, kt + BKV, S);
-    }
-    const bf16_t* sK = smem + (t & 1) * STAGE;
-    const bf16_t* sKt = sK + BKV * KP;
-    const bf16_t* sV = sKt + BKV * TP;
-    if (wq0 < S && !(a.causal && kt > wq1)) {
-      const bool diag = a.causal && kt + BKV - 1 > wq0;
+// dQ, plus delta_i = do_i . o_i for the dK/dV kernel (which runs after this one).
+template <int D>
+__global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int nitems) {
+  constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
+  static_assert(6 * DB * 16 * 64 * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int sub = w & 1, ph = w >> 1;
+  const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
+  const float c = a.scale * kLog2e;
+  float* cbuf = reinterpret_cast<float*>(smem);
+
+  for (int pass = 0; pass < 2; ++pass) {
+    const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
+    if (pass == 1 && item <= (int)blockIdx.x) break;
+    const Item it = item_q(item, BH, nqb);
+    const int b = it.bh / H, h = it.bh % H;
+    const int64_t tok0 = (int64_t)b * S;
+    const int wq0 = it.blk * 64 + 32 * sub, wq1 = wq0 + 31, q_row = wq0 + l32;
+    const bool qok = q_row < S;
+
+    bf16x8_t qreg[KS], doreg[KS];
+    load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, qok, g);
+    load_head_row<KS>(doreg, a.dout + (tok0 + q_row) * a.ld_do + (int64_t)h * D, qok, g);
+    float del = 0.f;
+    {
+      const bf16_t* op = a.o + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int i = 0; i < KS; ++i) {
+        if (!qok) break;
+        const u16x8_t ov = *reinterpret_cast<const u16x8_t*>(op + 16 * i + 8 * g);
+        const u16x8_t dv = __builtin_bit_cast(u16x8_t, doreg[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) del = fmaf(bf16_to_f32(ov[j]), bf16_to_f32(dv[j]), del);
+      }
+      del += __shfl_xor(del, 32, 64);
+    }
+    if (ph == 0 && g == 0 && qok) a.delta_out[(int64_t)it.bh * S + q_row] = del;
+    const float lse2 = qok ? a.lse[(int64_t)it.bh * S + q_row] * kLog2e : 0.f;
+    floatx16_t dqt[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) dqt[d] = zero16();
+
+    const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
+    const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
+    const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
+    const int nst = (kv_end + kStageRows - 1) / kStageRows;
+    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
+    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
+    wait_vm();
+    __syncthreads();
+    for (int t = 0; t < nst; ++t) {
+      if (t + 1 < nst) {
+        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+        dma_rows<D>(nxt, kbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
+        dma_rows<D>(nxt + TILE, vbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
+      }
+      const bf16_t* sK = smem + (t & 1) * 2 * TILE;
+      const bf16_t* sV = sK + TILE;
+      const int kt0 = t * kStageRows + 32 * ph;
+      if (wq0 < S && kt0 < kv_end && !(a.causal && kt0 > wq1)) {
         floatx16_t st = zero16(), dpt = zero16();
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-          st = mfma32(ld_frag(sK + (kb * 32 + l32) * KP + 16 * i + 8 * g), qreg[i], st);
-          dpt = mfma32(ld_frag(sV + (kb * 32 + l32) * KP + 16 * i + 8 * g), doreg[i], dpt);
+          st = mfma32(row_frag<D>(sK, 32 * ph, 16 * i, lane), qreg[i], st);
+          dpt = mfma32(row_frag<D>(sV, 32 * ph, 16 * i, lane), doreg[i], dpt);
         }
+        const bool diag = a.causal && kt0 + 31 > wq0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kt + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = key < S && q_row < S && !(diag && key > q_row);
-          const float p = ok ? exp2f(st[r] * c - lse2) : 0.f;
+          const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = qok && key < S && !(diag && key > q_row);
+          const float p = ok ? __builtin_amdgcn_exp2f(st[r] * c - lse2) : 0.f;
           st[r] = p * (dpt[r] - del);
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t dsb = pack8(st, s2);
 #pragma unroll
-          for (int d = 0; d < DB; ++d) dqt[d] = mfma32(tr_frag<TP>(sKt, kb * 32 + 16 * s2, d * 32, lane), dsb, dqt[d]);
+          for (int d = 0; d < DB; ++d) dqt[d] = mfma32(tr_frag<D>(sK, 32 * ph + 16 * s2, d * 32, lane), dsb, dqt[d]);
         }
       }
+      wait_vm();
+      __syncthreads();
     }
-    if (more) {
-      bf16_t* nK = smem + ((t + 1) & 1) * STAGE;
-      tk.template store<KP, TP>(nK, nK + BKV * KP);
-      tv.template store<KP, 0>(nK + BKV * KP + BKV * TP, nullptr);
+    merge_phases<0, DB>(cbuf, dqt, w, lane);
+    if (ph == 0 && qok) {
+      bf16_t* dqp = a.dq + (tok0 + q_row) * a.ld_d + (int64_t)h * D;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) st4(dqp + d * 32 + 8 * rr + 4 * g, dqt[d], rr, a.scale);
     }
-    __syncthreads();
   }
-  if (q_row >= S) return;
-  bf16_t* dqp = a.dq + (tok0 + q_row) * a.ld_d + (int64_t)h * D;
-#pragma unroll
-  for (int d = 0; d < DB; ++d)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) st4(dqp + d * 32 + 8 * rr + 4 * g, dqt[d], rr, a.scale);
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a) {
-  constexpr int BK = 128, BQT = 32, RP = Pitch<D>::ROW, TP = Pitch<D>::TR, KS = D / 16, DB = D / 32;
-  constexpr int STAGE = 2 * BQT * RP + 2 * BQT * TP;  // Q, dO (row reads); Q, dO (transpose reads)
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
-  __shared__ float sL[2][BQT], sDel[2][BQT];
+__global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, int nitems) {
+  constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (Q, dO)
+  __shared__ __attribute__((aligned(16))) bf16_t sVb[64 * D];          // the item's 64 rows of V
+  __shared__ __attribute__((aligned(16))) float sL[2][kStageRows];
+  __shared__ __attribute__((aligned(16))) float sDel[2][kStageRows];
+  static_assert(6 * DB * 16 * 64 * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int S = a.S, H = a.H;
-  const int kblk = blockIdx.x;  // block 0 has the most causal work; launched first
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int64_t tok0 = (int64_t)b * S;
-  const int wk0 = kblk * BK + w * 32;
-  const int key = wk0 + l32;
+  const int sub = w & 1, ph = w >> 1;
+  const int S = a.S, H = a.H, BH = a.B * a.H;
   const float c = a.scale * kLog2e;
+  float* cbuf = reinterpret_cast<float*>(smem);
 
-  bf16x8_t kreg[KS], vreg[KS];
-  {
-    const bf16_t* kp = a.k + (tok0 + key) * a.ld_qkv + (int64_t)h * D;
-    const bf16_t* vp = a.v + (tok0 + key) * a.ld_qkv + (int64_t)h * D;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
+    if (pass == 1 && item <= (int)blockIdx.x) break;
+    const Item it = item_k(item, BH);
+    const int b = it.bh / H, h = it.bh % H;
+    const int64_t tok0 = (int64_t)b * S;
+    const int wk0 = it.blk * 64 + 32 * sub;
+    const int key = wk0 + l32;
+
+    bf16x8_t kreg[KS];
+    load_head_row<KS>(kreg, a.k + (tok0 + key) * a.ld_qkv + (int64_t)h * D, key < S, g);
+    // V stays in LDS (registers are the binding limit at two waves per SIMD)
+    dma_rows<D, 64>(sVb, a.v + tok0 * a.ld_qkv + (int64_t)h * D, a.ld_qkv, it.blk * 64, S - 1, w, lane);
+    floatx16_t acc[2 * DB];  // dK^T blocks 0..DB-1, dV^T blocks DB..2DB-1
 #pragma unroll
-    for (int i = 0; i < KS; ++i) {
-      u16x8_t u = {0, 0, 0, 0, 0, 0, 0, 0}, v = u;
-      if (key < S) {
-        u = *reinterpret_cast<const u16x8_t*>(kp + 16 * i + 8 * g);
-        v = *reinterpret_cast<const u16x8_t*>(vp + 16 * i + 8 * g);
+    for (int d = 0; d < 2 * DB; ++d) acc[d] = zero16();
+
+    const bf16_t* qbase = a.q + tok0 * a.ld_qkv + (int64_t)h * D;
+    const bf16_t* dbase = a.dout + tok0 * a.ld_do + (int64_t)h * D;
+    const float* lse = a.lse + (int64_t)it.bh * S;
+    const float* dlt = a.delta + (int64_t)it.bh * S;
+    const int q_start = a.causal ? it.blk * 64 : 0;
+    const int nst = (S - q_start + kStageRows - 1) / kStageRows;
+    float l_pref = 0.f, d_pref = 0.f;
+    auto fetch_stats = [&](int q0) {
+      if (tid < kStageRows) {
+        const int q = q0 + tid;
+        l_pref = q < S ? lse[q] * kLog2e : 0.f;
+        d_pref = q < S ? dlt[q] : 0.f;
       }
-      kreg[i] = __builtin_bit_cast(bf16x8_t, u);
-      vreg[i] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-  floatx16_t dvt[DB], dkt[DB];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) {
-    dvt[d] = zero16();
-    dkt[d] = zero16();
-  }
-  const bf16_t* qbase = a.q + tok0 * a.ld_qkv + (int64_t)h * D;
-  const bf16_t* dbase = a.dout + tok0 * a.ld_do + (int64_t)h * D;
-  const int q_start = a.causal ? kblk * BK : 0;
-  const int ntiles = q_start < S ? (S - q_start + BQT - 1) / BQT : 0;
-  RowTile<D, BQT> tq, td;
-  float l_pref = 0.f, d_pref = 0.f;
-  auto load_tile = [&](int qt) {
-    tq.load(qbase, a.ld_qkv, qt, S);
-    td.load(dbase, a.ld_do, qt, S);
-    if (tid < BQT) {
-      const int q = qt + tid;
-      l_pref = q < S ? a.lse[(int64_t)bh * S + q] * kLog2e : 0.f;
-      d_pref = q < S ? a.delta[(int64_t)bh * S + q] : 0.f;
-    }
-  };
-  auto store_tile = [&](int stage) {
-    bf16_t* base = smem + stage * STAGE;
-    tq.template store<RP, TP>(base, base + 2 * BQT * RP);
-    td.template store<RP, TP>(base + BQT * RP, base + 2 * BQT * RP + BQT * TP);
-    if (tid < BQT) {
-      sL[stage][tid] = l_pref;
-      sDel[stage][tid] = d_pref;
-    }
-  };
-  if (ntiles > 0) {
-    load_tile(q_start);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int qt = q_start + t * BQT;
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(qt + BQT);
-    const int cur = t & 1;
-    const bf16_t* sQ = smem + cur * STAGE;
-    const bf16_t* sdO = sQ + BQT * RP;
-    const bf16_t* sQt = sQ + 2 * BQT * RP;
-    const bf16_t* sdOt = sQt + BQT * TP;
-    if (wk0 < S && !(a.causal && qt + BQT - 1 < wk0)) {
-      floatx16_t sc = zero16(), dp = zero16();
-#pragma unroll
-      for (int i = 0; i < KS; ++i) {
-        sc = mfma32(ld_frag(sQ + l32 * RP + 16 * i + 8 * g), kreg[i], sc);
-        dp = mfma32(ld_frag(sdO + l32 * RP + 16 * i + 8 * g), vreg[i], dp);
+    };
+    auto put_stats = [&](int stage) {
+      if (tid < kStageRows) {
+        sL[stage][tid] = l_pref;
+        sDel[stage][tid] = d_pref;
       }
-      const bool diag = a.causal && qt < wk0 + 31;  // some query in this tile precedes some key
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qi = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int q = qt + qi;
-        const bool ok = q < S && key < S && !(diag && key > q);
-        const float p = ok ? exp2f(sc[r] * c - sL[cur][qi]) : 0.f;
-        dp[r] = p * (dp[r] - sDel[cur][qi]);
-        sc[r] = p;
+    };
+    dma_rows<D>(smem, qbase, a.ld_qkv, q_start, S - 1, w, lane);
+    dma_rows<D>(smem + TILE, dbase, a.ld_do, q_start, S - 1, w, lane);
+    fetch_stats(q_start);
+    put_stats(0);
+    wait_vm();
+    __syncthreads();
+    for (int t = 0; t < nst; ++t) {
+      const int q0 = q_start + t * kStageRows;
+      if (t + 1 < nst) {
+        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+        dma_rows<D>(nxt, qbase, a.ld_qkv, q0 + kStageRows, S - 1, w, lane);
+        dma_rows<D>(nxt + TILE, dbase, a.ld_do, q0 + kStageRows, S - 1, w, lane);
+        fetch_stats(q0 + kStageRows);
       }
+      const int cur = t & 1;
+      const bf16_t* sQ = smem + cur * 2 * TILE;
+      const bf16_t* sdO = sQ + TILE;
+      const int qt0 = q0 + 32 * ph;
+      if (wk0 < S && qt0 < S && !(a.causal && qt0 + 31 < wk0)) {
+        floatx16_t sc = zero16(), dp = zero16();
+        // fragments are fetched one k-step ahead; the scheduling barriers keep the compiler from
+        // hoisting every LDS read of the stage (which would not fit the register budget)
+        bf16x8_t fq = row_frag<D>(sQ, 32 * ph, 0, lane), fd = row_frag<D>(sdO, 32 * ph, 0, lane),
+                 fv = row_frag<D>(sVb, 32 * sub, 0, lane);
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8_t pb = pack8(sc, s2), dsb = pack8(dp, s2);
+        for (int i = 0; i < KS; ++i) {
+          bf16x8_t nq = fq, nd = fd, nv = fv;
+          if (i + 1 < KS) {
+            nq = row_frag<D>(sQ, 32 * ph, 16 * (i + 1), lane);
+            nd = row_frag<D>(sdO, 32 * ph, 16 * (i + 1), lane);
+            nv = row_frag<D>(sVb, 32 * sub, 16 * (i + 1), lane);
+          }
+          sc = mfma32(fq, kreg[i], sc);
+          dp = mfma32(fd, fv, dp);
+          __builtin_amdgcn_sched_barrier(0);
+          fq = nq;
+          fd = nd;
+          fv = nv;
+        }
+        const bool diag = a.causal && qt0 < wk0 + 31;
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          dvt[d] = mfma32(tr_frag<TP>(sdOt, 16 * s2, d * 32, lane), pb, dvt[d]);
-          dkt[d] = mfma32(tr_frag<TP>(sQt, 16 * s2, d * 32, lane), dsb, dkt[d]);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int qi0 = 32 * ph + 8 * r4 + 4 * g;
+          const floatx4_t lq = *reinterpret_cast<const floatx4_t*>(&sL[cur][qi0]);
+          const floatx4_t dq4 = *reinterpret_cast<const floatx4_t*>(&sDel[cur][qi0]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * r4 + j;
+            const int q = q0 + qi0 + j;
+            const bool ok = q < S && key < S && !(diag && key > q);
+            const float p = ok ? __builtin_amdgcn_exp2f(sc[r] * c - lq[j]) : 0.f;
+            dp[r] = p * (dp[r] - dq4[j]);
+            sc[r] = p;
+          }
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8_t pb = pack8(sc, s2), dsb = pack8(dp, s2);
+          bf16x8_t fo = tr_frag<D>(sdO, 32 * ph + 16 * s2, 0, lane), fq2 = tr_frag<D>(sQ, 32 * ph + 16 * s2, 0, lane);
+#pragma unroll
+          for (int d = 0; d < DB; ++d) {
+            bf16x8_t no = fo, nq = fq2;
+            if (d + 1 < DB) {
+              no = tr_frag<D>(sdO, 32 * ph + 16 * s2, (d + 1) * 32, lane);
+              nq = tr_frag<D>(sQ, 32 * ph + 16 * s2, (d + 1) * 32, lane);
+            }
+            acc[DB + d] = mfma32(fo, pb, acc[DB + d]);
+            acc[d] = mfma32(fq2, dsb, acc[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            fo = no;
+            fq2 = nq;
+          }
         }
       }
+      if (t + 1 < nst) put_stats(cur ^ 1);
+      wait_vm();
+      __syncthreads();
     }
-    if (more) store_tile(cur ^ 1);
-    __syncthreads();
+    // merge dK^T then dV^T over the phases (the merge buffer holds DB accumulators per wave)
+    merge_phases<0, DB>(cbuf, acc, w, lane);
+    merge_phases<DB, DB>(cbuf, acc, w, lane);
+    if (ph == 0 && key < S) {
+      bf16_t* dkp = a.dk + (tok0 + key) * a.ld_d + (int64_t)h * D;
+      bf16_t* dvp = a.dv + (tok0 + key) * a.ld_d + (int64_t)h * D;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          st4(dkp + d * 32 + 8 * rr + 4 * g, acc[d], rr, a.scale);
+          st4(dvp + d * 32 + 8 * rr + 4 * g, acc[DB + d], rr, 1.f);
+        }
+    }
   }
-  if (key >= S) return;
-  bf16_t* dkp = a.dk + (tok0 + key) * a.ld_d + (int64_t)h * D;
-  bf16_t* dvp = a.dv + (tok0 + key) * a.ld_d + (int64_t)h * D;
-#pragma unroll
-  for (int d = 0; d < DB; ++d)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      st4(dkp + d * 32 + 8 * rr + 4 * g, dkt[d], rr, a.scale);
-      st4(dvp + d * 32 + 8 * rr + 4 * g, dvt[d], rr, 1.f);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -715,6 +785,8 @@ int check_common(int dtype, int64_t B, int64_t S, int64_t H, int64_t D) {
   RH_REQUIRE(D >= 1 && D <= 128, "rh_attn: head_dim %lld outside [1, 128]", (long long)D);
   RH_REQUIRE(S <= (1 << 24) && B * H <= 65535, "rh_attn: batch*heads %lld or seq %lld too large",
              (long long)(B * H), (long long)S);
+  RH_REQUIRE(B * H * ((S + 63) / 64) < INT32_MAX, "rh_attn: %lld x %lld row blocks exceed the launch limit",
+             (long long)(B * H), (long long)((S + 63) / 64));
   return RH_OK;
 }
 
@@ -735,6 +807,9 @@ AttnArgs<T> make_args(int64_t B, int64_t S, int64_t H, int64_t D, float scale, i
   a.causal = causal ? 1 : 0;
   return a;
 }
+
+// MFMA kernels: one item per (batch*head, 64-row block); each workgroup runs two items.
+int mfma_items(int64_t batch, int64_t seq, int64_t heads) { return (int)(batch * heads * ((seq + 63) / 64)); }
 
 template <typename T, int DMAX>
 void launch_generic_fwd(const AttnArgs<T>& a, hipStream_t st) {
@@ -771,9 +846,10 @@ extern "C" int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.ld_qkv = ld_qkv;
     a.o_out = (bf16_t*)o; a.ld_o = ld_o; a.lse_out = lse;
-    dim3 grid((unsigned)((seq + 127) / 128), (unsigned)(batch * heads));
-    if (head_dim == 64) hipLaunchKernelGGL(attn_fwd_mfma<64>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(attn_fwd_mfma<128>, grid, dim3(256), 0, st, a);
+    const int nitems = mfma_items(batch, seq, heads);
+    dim3 grid((unsigned)((nitems + 1) / 2));
+    if (head_dim == 64) hipLaunchKernelGGL(attn_fwd_mfma<64>, grid, dim3(512), 0, st, a, nitems);
+    else hipLaunchKernelGGL(attn_fwd_mfma<128>, grid, dim3(512), 0, st, a, nitems);
     return rh_check_launch("rh_attn_fwd");
   }
   if (dtype == RH_DTYPE_BF16) {
@@ -820,24 +896,19 @@ extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
     a.o = (const bf16_t*)o; a.ld_o = ld_o; a.dout = (const bf16_t*)dout; a.ld_do = ld_do;
     a.lse = lse; a.delta = delta; a.delta_out = delta;
     a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv; a.ld_d = ld_dqkv;
-    if (mfma_ok(dtype, head_dim, {o, dout}, {ld_o, ld_do})) {
-      const unsigned vblocks = (unsigned)((rows * (head_dim / 8) + 255) / 256);
-      if (head_dim == 64) hipLaunchKernelGGL(attn_delta_vec<64>, dim3(vblocks), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL(attn_delta_vec<128>, dim3(vblocks), dim3(256), 0, st, a);
-    } else {
-      hipLaunchKernelGGL(attn_delta<bf16_t>, dim3(dblocks), dim3(256), 0, st, a);
-    }
-    if (mfma_ok(dtype, head_dim, {q, k, v, dout, dq, dk, dv}, {ld_qkv, ld_do, ld_dqkv})) {
-      dim3 gq((unsigned)((seq + 127) / 128), (unsigned)(batch * heads));
-      dim3 gk((unsigned)((seq + 127) / 128), (unsigned)(batch * heads));
+    if (mfma_ok(dtype, head_dim, {q, k, v, o, dout, dq, dk, dv}, {ld_qkv, ld_o, ld_do, ld_dqkv})) {
+      // the dQ kernel also writes delta, which the dK/dV kernel reads
+      const int nitems = mfma_items(batch, seq, heads);
+      dim3 grid((unsigned)((nitems + 1) / 2));
       if (head_dim == 64) {
-        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<64>, gk, dim3(256), 0, st, a);
-        hipLaunchKernelGGL(attn_bwd_dq_mfma<64>, gq, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(attn_bwd_dq_mfma<64>, grid, dim3(512), 0, st, a, nitems);
+        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<64>, grid, dim3(512), 0, st, a, nitems);
       } else {
-        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<128>, gk, dim3(256), 0, st, a);
-        hipLaunchKernelGGL(attn_bwd_dq_mfma<128>, gq, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(attn_bwd_dq_mfma<128>, grid, dim3(512), 0, st, a, nitems);
+        hipLaunchKernelGGL(attn_bwd_dkdv_mfma<128>, grid, dim3(512), 0, st, a, nitems);
       }
     } else {
+      hipLaunchKernelGGL(attn_delta<bf16_t>, dim3(dblocks), dim3(256), 0, st, a);
       dispatch_generic(a, st, false);
     }
   } else {

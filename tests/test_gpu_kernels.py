@@ -153,6 +153,9 @@ def _attn_ref(q, k, v, heads):
     (torch.bfloat16, 128, 200, 1, 1),
     (torch.bfloat16, 64, 320, 3, 2),
     (torch.bfloat16, 64, 1024, 2, 1),
+    (torch.bfloat16, 128, 2048, 2, 2),
+    (torch.bfloat16, 128, 1000, 3, 1),
+    (torch.bfloat16, 64, 63, 1, 3),
     (torch.bfloat16, 32, 96, 2, 2),
     (torch.float32, 16, 32, 4, 4),
     (torch.float32, 64, 130, 2, 1),
