@@ -279,6 +279,91 @@ __device__ __forceinline__ void mma_ktile(const bf16_t* a_s, const bf16_t* b_s, 
   }
 }
 
+// Epilogue through LDS: the fp32 tile is written to LDS in row chunks, then every thread takes
+// 8 consecutive columns at a time -- one rolled loop, 16-byte coalesced loads and stores.
+// 32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// `smem_elems` bf16 elements of LDS are free for it (the caller's stages, after a barrier).
+template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int SMEM_ELEMS, int FM, int FN>
+__device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, bf16_t* smem, floatx16_t (&acc)[FM][FN],
+                                                   int64_t m0, int64_t n0, int wm, int wn, int lane) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int CP = BN >= 256 ? BN : BN + 4;                 // fp32 row pitch in LDS
+  constexpr int CH_MAX = (SMEM_ELEMS * (int)sizeof(bf16_t)) / (CP * 4);
+  constexpr int CH = CH_MAX >= BM ? BM : (CH_MAX >= WTM ? (CH_MAX / WTM) * WTM : WTM);
+  static_assert(CH * CP * 4 <= SMEM_ELEMS * (int)sizeof(bf16_t), "epilogue chunk must fit the LDS stages");
+  float* cs = reinterpret_cast<float*>(smem);
+  const int g = lane >> 5, c32 = lane & 31;
+  for (int r0 = 0; r0 < BM; r0 += CH) {
+    // waves whose rows fall in [r0, r0 + CH) deposit their accumulators
+    if (wm * WTM >= r0 && wm * WTM < r0 + CH) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * WTM - r0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            cs[row * CP + wn * WTN + j * 32 + c32] = acc[i][j][r];
+          }
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int e = threadIdx.x; e < CH * (BN / 8); e += NT) {
+      const int row = e / (BN / 8), col = (e % (BN / 8)) * 8;
+      const int64_t m = m0 + r0 + row, n = n0 + col;
+      if (m >= p.M || n >= p.N) continue;
+      const floatx4_t lo = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col);
+      const floatx4_t hi = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col + 4);
+      float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if (SPLIT) {
+        float* w = p.ws + (int64_t)blockIdx.z * p.M * p.N + m * p.N + n;
+        if (n + 8 <= p.N && p.N % 4 == 0) {
+          *reinterpret_cast<floatx4_t*>(w) = lo;
+          *reinterpret_cast<floatx4_t*>(w + 4) = hi;
+        } else {
+          for (int t = 0; t < 8 && n + t < p.N; ++t) w[t] = v[t];
+        }
+        continue;
+      }
+      bf16_t* dp = d_row(p, m) + n;
+      const bf16_t* cp = p.C ? p.C + m * p.ldc + n : dp;
+      const bf16_t* xp = EPI == RH_EPI_GELU ? p.aux_out + m * p.ldaux + n
+                                            : (EPI == RH_EPI_GELU_GRAD ? p.aux + m * p.ldaux + n : dp);
+      const bool vec = n + 8 <= p.N && (((uintptr_t)dp | (uintptr_t)xp) & 15) == 0 &&
+                       (p.beta == 0.f || ((uintptr_t)cp & 15) == 0);
+      if (vec) {
+        if (p.beta != 0.f) {
+          const u16x8_t c = *reinterpret_cast<const u16x8_t*>(cp);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = p.alpha * v[t] + p.beta * bf16_to_f32(c[t]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
+        }
+        u16x8_t o;
+        if (EPI == RH_EPI_GELU) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+          *reinterpret_cast<u16x8_t*>(const_cast<bf16_t*>(xp)) = o;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
+        } else if (EPI == RH_EPI_GELU_GRAD) {
+          const u16x8_t a = *reinterpret_cast<const u16x8_t*>(xp);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+        *reinterpret_cast<u16x8_t*>(dp) = o;
+      } else {
+        for (int t = 0; t < 8 && n + t < p.N; ++t) epilogue_store<bf16_t, EPI>(p, m, n + t, v[t]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16_t> p) {
   constexpr int NT = 64 * WGM * WGN;
@@ -375,84 +460,245 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16
     }
   }
 
-  // Epilogue through LDS: the fp32 tile is written to LDS in row chunks, then every thread
-  // takes 8 consecutive columns at a time -- one rolled loop, 16-byte coalesced loads and
-  // stores.  32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32.
-  constexpr int CP = BN >= 256 ? BN : BN + 4;                 // fp32 row pitch in LDS
-  constexpr int CH_MAX = (2 * STAGE * (int)sizeof(bf16_t)) / (CP * 4);
-  constexpr int CH = CH_MAX >= BM ? BM : (CH_MAX >= WTM ? (CH_MAX / WTM) * WTM : WTM);
-  static_assert(CH * CP * 4 <= 2 * STAGE * (int)sizeof(bf16_t), "epilogue chunk must fit the LDS stages");
-  float* cs = reinterpret_cast<float*>(smem);
-  const int g = lane >> 5, c32 = lane & 31;
-  for (int r0 = 0; r0 < BM; r0 += CH) {
-    // waves whose rows fall in [r0, r0 + CH) deposit their accumulators
-    if (wm * WTM >= r0 && wm * WTM < r0 + CH) {
+  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+}
+
+
+// ---------------------------------------------------------------------------
+// bf16 MFMA kernel, pipelined: NST-stage LDS ring fed by direct global->LDS loads
+// ---------------------------------------------------------------------------
+// k-tile 32, NST = 5 stages for 256x256 tiles (160 KB).  Iteration t issues the loads of tile
+// t+NST-1 (global_load_lds_dwordx4: no staging registers, no LDS write instructions), runs the
+// two k-steps of tile t from registers while reading the next fragments, and reads tile t+1's
+// first fragments before the barrier that ends the iteration -- so the MFMA pipe has work
+// queued across every barrier.  The barrier publishes tile t+2 (each thread first waits for its
+// own loads of that tile, leaving up to NST-3 younger tiles in flight: the loads are
+// latency-bound, so depth is throughput) and frees stage t for tile t+NST.  Needs: bf16, 16-byte aligned rows, K per split a multiple of 32, m/n-
+// contiguous operand extents a multiple of 8, segment boundaries a multiple of 32 k-rows.
+// Rows / columns past the matrix edge are clamped onto the last valid ones (their results
+// are never stored).
+constexpr int dBK = 32;
+
+// LDS ring depth per tile shape: as many 32-deep stages as the LDS budget holds (at most 6);
+// 128x128 tiles keep to 80 KB so that two workgroups share a CU
+template <int BM, int BN>
+constexpr int dma_stages() {
+  constexpr int budget = (BM == 128 && BN == 128) ? 80 * 1024 : 160 * 1024;
+  constexpr int n = budget / ((BM + BN) * dBK * 2);
+  return n > 6 ? 6 : n;
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// element offset of (row r, 16-byte chunk c) in a k-contiguous [R][32] tile: 64-byte rows,
+// chunk c stored at c ^ ((r >> 2) & 3), so 16 consecutive rows hit 16 distinct bank groups
+__device__ __forceinline__ int kc32_off(int r, int c) { return r * dBK + ((c ^ ((r >> 2) & 3)) << 3); }
+
+template <int ROWS, bool KC>
+__device__ __forceinline__ bf16x8_t load_frag32(const bf16_t* s, int rb, int ks, int lane) {
+  if (KC) {
+    const int r = rb + (lane & 31);
+    return *reinterpret_cast<const bf16x8_t*>(s + kc32_off(r, ks * 2 + (lane >> 5)));
+  }
+  return load_frag<ROWS, false>(s, rb, ks, lane);
+}
+
+// Direct global->LDS load of 16 bytes per lane: lane l of the wave writes LDS bytes
+// lds_base + 16*l .. +15 (lds_base wave-uniform).  Issued through inline asm on purpose: the
+// compiler cannot see that the asynchronous LDS write never aliases the stages being read, and
+// with the builtin it waits for every outstanding load before each LDS read, serialising the
+// pipeline.  Completion is tracked explicitly with wait_vm_le (these loads count in vmcnt).
+__device__ __forceinline__ void dma16(const bf16_t* src, const bf16_t* lds_dst) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(lds)
+      : "memory", "m0");
+}
+
+// One operand's share of a k-tile, issued as 1 KB direct-to-LDS windows (lane l of a window
+// lands at window byte 16*l).  KC: window = 16 rows x 4 chunks; !KC: window = 512/ROWS k-rows.
+template <int ROWS, bool KC, int NWAVES>
+struct DmaOperand {
+  static constexpr int WIN = ROWS * dBK * 2 / 1024;
+  static constexpr int PER = WIN / NWAVES;
+  static_assert(WIN % NWAVES == 0, "tile windows must split evenly over the waves");
+  static constexpr int KROWS = 512 / ROWS;  // !KC: k-rows per window
+  // KC: per-lane row pointers (advanced by dBK per tile); !KC: per-lane element offset from the
+  // k-tile's first row (k-row within the tile * ld + column)
+  const bf16_t* rowp[PER];
+  int64_t off[PER];
+
+  template <typename RowFn>
+  __device__ __forceinline__ void setup(RowFn rowptr, int64_t o0, int64_t extent, int64_t kbeg, int64_t ld, int wave,
+                                        int lane) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = wm * WTM - r0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            cs[row * CP + wn * WTN + j * 32 + c32] = acc[i][j][r];
-          }
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int e = threadIdx.x; e < CH * (BN / 8); e += NT) {
-      const int row = e / (BN / 8), col = (e % (BN / 8)) * 8;
-      const int64_t m = m0 + r0 + row, n = n0 + col;
-      if (m >= p.M || n >= p.N) continue;
-      const floatx4_t lo = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col);
-      const floatx4_t hi = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col + 4);
-      float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      if (SPLIT) {
-        float* w = p.ws + (int64_t)blockIdx.z * p.M * p.N + m * p.N + n;
-        if (n + 8 <= p.N && p.N % 4 == 0) {
-          *reinterpret_cast<floatx4_t*>(w) = lo;
-          *reinterpret_cast<floatx4_t*>(w + 4) = hi;
-        } else {
-          for (int t = 0; t < 8 && n + t < p.N; ++t) w[t] = v[t];
-        }
-        continue;
-      }
-      bf16_t* dp = d_row(p, m) + n;
-      const bf16_t* cp = p.C ? p.C + m * p.ldc + n : dp;
-      const bf16_t* xp = EPI == RH_EPI_GELU ? p.aux_out + m * p.ldaux + n
-                                            : (EPI == RH_EPI_GELU_GRAD ? p.aux + m * p.ldaux + n : dp);
-      const bool vec = n + 8 <= p.N && (((uintptr_t)dp | (uintptr_t)xp) & 15) == 0 &&
-                       (p.beta == 0.f || ((uintptr_t)cp & 15) == 0);
-      if (vec) {
-        if (p.beta != 0.f) {
-          const u16x8_t c = *reinterpret_cast<const u16x8_t*>(cp);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] = p.alpha * v[t] + p.beta * bf16_to_f32(c[t]);
-        } else {
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
-        }
-        u16x8_t o;
-        if (EPI == RH_EPI_GELU) {
-#pragma unroll
-          for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
-          *reinterpret_cast<u16x8_t*>(const_cast<bf16_t*>(xp)) = o;
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
-        } else if (EPI == RH_EPI_GELU_GRAD) {
-          const u16x8_t a = *reinterpret_cast<const u16x8_t*>(xp);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
-        *reinterpret_cast<u16x8_t*>(dp) = o;
+    for (int i = 0; i < PER; ++i) {
+      const int win = wave + NWAVES * i;
+      if (KC) {
+        const int row = win * 16 + lane / 4;
+        const int lchunk = (lane & 3) ^ ((row >> 2) & 3);
+        const int64_t gr = min(o0 + row, extent - 1);
+        rowp[i] = rowptr(gr) + kbeg + lchunk * 8;
       } else {
-        for (int t = 0; t < 8 && n + t < p.N; ++t) epilogue_store<bf16_t, EPI>(p, m, n + t, v[t]);
+        const int kr = win * KROWS + lane / (ROWS / 8);
+        const int pchunk = lane % (ROWS / 8);
+        const int lunit = (pchunk >> 2) ^ (kr & 3);
+        const int64_t c = o0 + lunit * 32 + (pchunk & 3) * 8;
+        off[i] = (int64_t)kr * ld + min(c, extent - 8);
       }
     }
+  }
+
+  // issue tile kt into LDS tile `dst`; `krow0` = pointer to the tile's first k-row (!KC)
+  __device__ __forceinline__ void issue(bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int win = wave + NWAVES * i;
+      dma16(KC ? rowp[i] + (int64_t)kt * dBK : krow0 + off[i], dst + win * 512);
+    }
+  }
+};
+
+// wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
+// outstanding; they complete in issue order
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_t> p) {
+  constexpr int NW = WGM * WGN;
+  constexpr bool A_KC = (L != RH_GEMM_TN);
+  constexpr bool B_KC = (L == RH_GEMM_NT);
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_ELEMS = BM * dBK, B_ELEMS = BN * dBK, STAGE = A_ELEMS + B_ELEMS;
+  constexpr int NST = dma_stages<BM, BN>();
+  static_assert(NST >= 4, "the pipeline needs at least four stages");
+  using DA = DmaOperand<BM, A_KC, NW>;
+  using DB = DmaOperand<BN, B_KC, NW>;
+  constexpr int PT = DA::PER + DB::PER;  // loads per thread per k-tile
+  __shared__ __attribute__((aligned(16))) bf16_t smem[NST * STAGE];
+
+  int tm, tn;
+  tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t kbeg = (int64_t)blockIdx.z * p.k_per_split;
+  const int64_t kend = min(p.K, kbeg + p.k_per_split);
+  const int nk = (int)((kend - kbeg) / dBK);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  DA da;
+  DB db;
+  da.setup([&](int64_t r) { return p.A + r * p.lda; }, m0, p.M, kbeg, p.lda, wave, lane);
+  db.setup([&](int64_t r) { return b_row(p, r); }, n0, p.N, kbeg, p.ldb, wave, lane);
+  // B segments of an m/n-contiguous B (k-rows split over up to RH_MAX_SEG tensors): a k-tile
+  // never straddles one, so the issuing side tracks (segment, row in segment) as it advances --
+  // no division and no kernel-argument load inside the loop.
+  // (All of it uniform, kept in scalar registers: 32-bit row counters, a select chain rather
+  // than an indexed array.)
+  const bf16_t* const bs0 = p.B[0];
+  const bf16_t* const bs1 = p.B[1 % RH_MAX_SEG];
+  const bf16_t* const bs2 = p.B[2 % RH_MAX_SEG];
+  const bf16_t* const bs3 = p.B[3 % RH_MAX_SEG];
+  static_assert(RH_MAX_SEG == 4, "segment select assumes four B pointers");
+  const int bseg_rows = (!B_KC && p.b_nseg > 1) ? (int)p.b_seg : INT32_MAX;
+  int iss_seg = 0, iss_row = (int)kbeg;  // segment and row-in-segment of the next tile to issue
+  if (!B_KC && p.b_nseg > 1) {
+    iss_seg = (int)kbeg / bseg_rows;
+    iss_row = (int)kbeg - iss_seg * bseg_rows;
+  }
+  auto issue = [&](int kt) {
+    bf16_t* st = smem + (kt % NST) * STAGE;
+    const int64_t k0 = kbeg + (int64_t)kt * dBK;
+    da.issue(st, kt, A_KC ? nullptr : p.A + k0 * p.lda, wave);
+    if (B_KC) {
+      db.issue(st + A_ELEMS, kt, nullptr, wave);
+    } else {
+      const bf16_t* base = iss_seg == 0 ? bs0 : iss_seg == 1 ? bs1 : iss_seg == 2 ? bs2 : bs3;
+      db.issue(st + A_ELEMS, kt, base + (int64_t)iss_row * p.ldb, wave);
+      iss_row += dBK;
+      if (iss_row >= bseg_rows) {
+        iss_row -= bseg_rows;
+        ++iss_seg;
+      }
+    }
+  };
+
+  floatx16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  bf16x8_t fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+  auto read_frags = [&](bf16x8_t(&fa)[FM], bf16x8_t(&fb)[FN], int kt, int ks) {
+    const bf16_t* st = smem + (kt % NST) * STAGE;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[i] = load_frag32<BM, A_KC>(st, wm * WTM + i * 32, ks, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[j] = load_frag32<BN, B_KC>(st + A_ELEMS, wn * WTN + j * 32, ks, lane);
+  };
+  auto mma = [&](const bf16x8_t(&fa)[FM], const bf16x8_t(&fb)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+
+  // wait until tile `need` has landed, given that tiles up to `issued` have been issued
+  auto wait_tile = [&](int need, int issued) {
+    const int younger = issued - need;  // tiles allowed in flight
+    if (younger >= 3) wait_vm_le<3 * PT>();
+    else if (younger == 2) wait_vm_le<2 * PT>();
+    else if (younger == 1) wait_vm_le<PT>();
+    else wait_vm_le<0>();
+  };
+  if (nk > 0) {
+    const int pro = min(nk, NST - 1);
+    for (int t = 0; t < pro; ++t) issue(t);
+    // iteration 0 reads tiles 0 and 1
+    wait_tile(min(1, nk - 1), pro - 1);
+    __syncthreads();
+    read_frags(fa0, fb0, 0, 0);
+  }
+  // LDS instructions per fragment set (a transposed fragment takes two reads)
+  constexpr int NREAD = FM * (A_KC ? 1 : 2) + FN * (B_KC ? 1 : 2);
+#pragma unroll 1
+  for (int kt = 0; kt < nk; ++kt) {
+    const int nxt = kt + NST - 1;
+    if (nxt < nk) issue(nxt);
+    // every read of the next fragment set is issued before the MFMAs on the current one, so
+    // the LDS latency hides behind FM*FN MFMAs (the scheduler would otherwise recycle the
+    // current set's registers and serialise them)
+    read_frags(fa1, fb1, kt, 1);
+    mma(fa0, fb0);
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // unconditional (the last iteration reads a stale stage it never uses): a branch here would
+    // make the wait-count pass merge both paths and over-wait on the next tile's reads
+    read_frags(fa0, fb0, kt + 1, 0);
+    mma(fa1, fb1);
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // tile kt+2 must have landed before the barrier publishes it; younger tiles may still fly
+    wait_tile(min(kt + 2, nk - 1), min(nxt, nk - 1));
     __syncthreads();
   }
+
+  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, NST * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -533,6 +779,48 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmParams<T> p, int s
     float s = 0.f;
     for (int z = 0; z < splits; ++z) s += p.ws[(int64_t)z * total + idx];
     epilogue_store<T, EPI>(p, idx / p.N, idx % p.N, s);
+  }
+}
+
+// bf16, N % 8 == 0, 16-byte aligned rows: each thread reduces 8 consecutive outputs with
+// 16-byte partial loads (the partials are read exactly once) and one 16-byte store.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_vec(GemmParams<bf16_t> p, int splits) {
+  const int64_t total8 = p.M * p.N / 8;
+  const int64_t n8 = p.N / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total8; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / n8, n = (i - m * n8) * 8;
+    floatx4_t lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    for (int z = 0; z < splits; ++z) {
+      const float* w = p.ws + (int64_t)z * p.M * p.N + m * p.N + n;
+      lo += *reinterpret_cast<const floatx4_t*>(w);
+      hi += *reinterpret_cast<const floatx4_t*>(w + 4);
+    }
+    float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    bf16_t* dp = d_row(p, m) + n;
+    if (p.beta != 0.f) {
+      const u16x8_t c = *reinterpret_cast<const u16x8_t*>(p.C ? p.C + m * p.ldc + n : dp);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = p.alpha * v[t] + p.beta * bf16_to_f32(c[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
+    }
+    u16x8_t o;
+    if (EPI == RH_EPI_GELU) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+      *reinterpret_cast<u16x8_t*>(p.aux_out + m * p.ldaux + n) = o;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
+    } else if (EPI == RH_EPI_GELU_GRAD) {
+      const u16x8_t a = *reinterpret_cast<const u16x8_t*>(p.aux + m * p.ldaux + n);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
+    *reinterpret_cast<u16x8_t*>(dp) = o;
   }
 }
 
@@ -678,23 +966,41 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
 }
 
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
-void launch_bf16(const GemmParams<bf16_t>& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
+void launch_bf16(const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t st) {
+  if (dma) hipLaunchKernelGGL((gemm_bf16_dma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
+  else hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
 }
 
 template <int L, int EPI, bool SPLIT>
-void launch_cfg(int cfg, const GemmParams<bf16_t>& p, dim3 grid, hipStream_t st) {
+void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t st) {
   switch (cfg) {
-    case kT256x256: launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, grid, st); break;
-    case kT256x128: launch_bf16<256, 128, 4, 2, L, EPI, SPLIT>(p, grid, st); break;
-    default: launch_bf16<128, 128, 2, 2, L, EPI, SPLIT>(p, grid, st); break;
+    case kT256x256: launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st); break;
+    case kT256x128: launch_bf16<256, 128, 4, 2, L, EPI, SPLIT>(p, dma, grid, st); break;
+    default: launch_bf16<128, 128, 2, 2, L, EPI, SPLIT>(p, dma, grid, st); break;
   }
 }
 
+// The pipelined direct-to-LDS kernel covers every call whose operands it can address without
+// bounds checks (see gemm_bf16_dma); RESIHP_GEMM_DMA=0 forces the register-staged kernel.
+bool dma_ok(const rh_gemm_desc* d, const Plan& pl, const GemmParams<bf16_t>& p) {
+  static const int enabled = [] {
+    const char* e = getenv("RESIHP_GEMM_DMA");
+    return (e && e[0] == '0' && e[1] == 0) ? 0 : 1;
+  }();
+  if (!enabled || !p.aligned || d->K % dBK || pl.k_per_split % dBK) return false;
+  // measured on MI355X: faster for NT and NN, slower than the register-staged kernel for TN
+  if (d->layout == RH_GEMM_TN) return false;
+  const bool a_kc = d->layout != RH_GEMM_TN, b_kc = d->layout == RH_GEMM_NT;
+  if (!a_kc && (d->M < 8 || d->M % 8)) return false;
+  if (!b_kc && (d->N < 8 || d->N % 8)) return false;
+  if (!b_kc && d->b_nseg > 1 && d->b_seg_rows % dBK) return false;
+  return true;
+}
+
 template <typename T, int L, int EPI, bool SPLIT>
-void launch_main(int cfg, const GemmParams<T>& p, dim3 grid, hipStream_t st) {
+void launch_main(int cfg, const GemmParams<T>& p, bool dma, dim3 grid, hipStream_t st) {
   if constexpr (std::is_same<T, bf16_t>::value) {
-    launch_cfg<L, EPI, SPLIT>(cfg, p, grid, st);
+    launch_cfg<L, EPI, SPLIT>(cfg, p, dma, grid, st);
   } else {
     hipLaunchKernelGGL((gemm_f32_fma<L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
   }
@@ -706,17 +1012,34 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
   const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
   if (tiles > INT32_MAX) return rh_set_error(RH_ERR_INVALID, "rh_gemm: too many tiles (%lld)", (long long)tiles);
   dim3 grid((unsigned)tiles, 1, (unsigned)pl.splits);
+  bool dma = false;
+  if constexpr (std::is_same<T, bf16_t>::value) dma = dma_ok(d, pl, p);
   if (pl.splits > 1) {
-    launch_main<T, L, EPI, true>(pl.cfg, p, grid, st);
+    launch_main<T, L, EPI, true>(pl.cfg, p, dma, grid, st);
     int rc = rh_check_launch("rh_gemm");
     if (rc) return rc;
     const int64_t total = d->M * d->N;
+    if constexpr (std::is_same<T, bf16_t>::value) {
+      // every output row and the partials are 16-byte aligned when N % 8 == 0 (the partials
+      // are [splits][M][N] fp32); D/C/aux rows need ld % 8 == 0 and aligned bases as well
+      bool vec = d->N % 8 == 0 && d->ldd % 8 == 0 && rh_aligned(ws, 16);
+      for (int q = 0; q < d->d_nseg; ++q) vec = vec && rh_aligned(d->D[q], 16);
+      if (d->beta != 0.f && d->C) vec = vec && rh_aligned(d->C, 16) && d->ldc % 8 == 0;
+      if (d->epilogue != RH_EPI_NONE)
+        vec = vec && rh_aligned(d->epilogue == RH_EPI_GELU ? d->aux_out : d->aux, 16) && d->ldaux % 8 == 0;
+      if (vec) {
+        int64_t blocks = rh_cdiv(total / 8, 256);
+        if (blocks > 8 * 1024) blocks = 8 * 1024;
+        hipLaunchKernelGGL((gemm_splitk_reduce_vec<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
+        return rh_check_launch("rh_gemm split-k reduce");
+      }
+    }
     int64_t blocks = rh_cdiv(total, 256);
     if (blocks > 4 * 1024) blocks = 4 * 1024;
     hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
     return rh_check_launch("rh_gemm split-k reduce");
   }
-  launch_main<T, L, EPI, false>(pl.cfg, p, grid, st);
+  launch_main<T, L, EPI, false>(pl.cfg, p, dma, grid, st);
   return rh_check_launch("rh_gemm");
 }
 
