@@ -870,12 +870,14 @@ Plan plan_gemm(const rh_gemm_desc* d) {
     const int64_t tiles = tm * tn;
     const int64_t per_cu = c == kT128x128 ? 2 : 1;  // co-resident workgroups (LDS-bound)
     const int64_t slots = cus * per_cu;
-    for (int64_t splits = 1; splits <= 8; splits *= 2) {
-      if (splits > 1 && (d->K / splits < 512 || tiles * (splits / 2) >= slots)) break;
+    for (int64_t splits = 1; splits <= 8; ++splits) {
+      if (splits > 1 && (d->K / splits < 512 || tiles * (splits - 1) >= slots)) break;
       const int64_t kps = rh_cdiv(rh_cdiv(d->K, splits), kBK) * kBK;
       const int64_t waves = rh_cdiv(tiles * splits, slots);
       double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / kTileEff[c];
-      if (splits > 1) t += 4.0 * (double)splits * d->M * d->N / 64.0;  // partial write + reduce traffic
+      // partial write + reduce: measured on MI355X, a split-4 2048x2048 reduce costs ~1/4 of a
+      // 256x256x2048 tile wave, i.e. ~2 units per partial element
+      if (splits > 1) t += 2.0 * (double)splits * d->M * d->N;
       if (t < best * 0.98) {
         best = t;
         pl.cfg = c;
