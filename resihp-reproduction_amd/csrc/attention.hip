@@ -308,24 +308,56 @@ __device__ __forceinline__ int swz(int r, int c) {
   return r * D + ((((c >> 3) ^ sw)) << 3) + (c & 7);
 }
 
-// Operand fragment of rows r0 + lane%32, eight columns c0 + 8*(lane/32).. (ds_read_b128).
+// Fragment reads by byte address.  In a swizzled tile row r starts at byte 2*D*r, and for the
+// fragment shapes below the column-dependent part of the address is a per-lane base XORed
+// with a compile-time constant (the k-step / head-dim block), because the swizzle XOR acts
+// on the same address bits the constant selects.  Each lane therefore keeps one base per read
+// pattern, and a read costs one v_xor on top of (stage base + row block): no per-fragment
+// address registers.  Bases: row fragments -> row_base, transposed fragments -> tr_base(0/1).
 template <int D>
-__device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int c0, int lane) {
-  return *reinterpret_cast<const bf16x8_t*>(tile + swz<D>(r0 + (lane & 31), c0 + 8 * (lane >> 5)));
+__device__ __forceinline__ int swz_bits(int r) {
+  return D == 128 ? (4 * (r & 3) + ((r >> 2) & 3)) : (4 * ((r >> 1) & 1) + ((r >> 2) & 3));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+template <int D>
+struct FragAddr {
+  uint32_t row;    // row fragment: row l%32, chunk 2i + l/32
+  uint32_t tr[2];  // transposed fragment, lo (rows 4g + i/4) and hi (+8) reads
+  __device__ __forceinline__ explicit FragAddr(int lane) {
+    const int g = lane >> 5, l32 = lane & 31;
+    row = (uint32_t)(2 * D * l32 + 16 * (g ^ swz_bits<D>(l32)));
+    const int q = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rl = 4 * (q >> 1) + (i >> 2) + 8 * h;
+      const int x = swz_bits<D>(rl) ^ (2 * (q & 1) + ((i & 3) >> 1));
+      tr[h] = (uint32_t)(2 * D * rl + 16 * x + 8 * (i & 1));
+    }
+  }
+};
+
+// Operand fragment of rows r0 + lane%32 (r0 a multiple of 16), eight columns 16*ks + 8*(lane/32)
+// (ds_read_b128).  `tile` is 256-byte aligned.
+template <int D>
+__device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int ks, const FragAddr<D>& fa) {
+  const uint32_t a = (lds_addr(tile) + (uint32_t)(2 * D * r0) + fa.row) ^ (uint32_t)(32 * ks);
+  return *(const __attribute__((address_space(3))) bf16x8_t*)(uintptr_t)a;
 }
 
-// Transposed operand fragment: rows of the MFMA operand are the 32 tile columns c0..c0+31,
+// Transposed operand fragment: rows of the MFMA operand are the 32 tile columns 32*db..+31,
 // its eight k values are the tile rows r0 + {4g..4g+3, 8+4g..8+4g+3} (g = lane/32) -- the k
 // order of accumulator registers 8s..8s+7.  Two ds_read_b64_tr_b16: in each 16-lane block,
-// lane i addresses tile row r0 + 4g + i/4 (+8), columns c0 + 16*(block&1) + 4*(i%4)..+3, and
-// lane j receives those four rows of column c0 + 16*(block&1) + j.
+// lane i addresses tile row r0 + 4g + i/4 (+8), columns 32*db + 16*(block&1) + 4*(i%4)..+3,
+// and lane j receives those four rows of column 32*db + 16*(block&1) + j.
 template <int D>
-__device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int c0, int lane) {
-  const int q = lane >> 4, i = lane & 15, g = q >> 1;
-  const int col = c0 + 16 * (q & 1) + 4 * (i & 3);
-  const int row = r0 + 4 * g + (i >> 2);
-  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + swz<D>(row, col)));
-  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + swz<D>(row + 8, col)));
+__device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int db, const FragAddr<D>& fa) {
+  const uint32_t base = lds_addr(tile) + (uint32_t)(2 * D * r0);
+  const uint32_t a0 = (base + fa.tr[0]) ^ (uint32_t)(64 * db);
+  const uint32_t a1 = (base + fa.tr[1]) ^ (uint32_t)(64 * db);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(uintptr_t)a0);
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(uintptr_t)a1);
   s16x4_t both[2] = {lo, hi};
   return __builtin_bit_cast(bf16x8_t, both);
 }
@@ -416,10 +448,11 @@ __device__ __forceinline__ void merge_phases(float* cbuf, floatx16_t (&acc)[N], 
 template <int D>
 __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nitems) {
   constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
+  __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
   static_assert((6 * DB * 16 * 64 + 1024) * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int sub = w & 1, ph = w >> 1;
+  const FragAddr<D> fa(lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
   float* cbuf = reinterpret_cast<float*>(smem);
@@ -459,7 +492,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
       if (wq0 < S && kt0 < kv_end && !(a.causal && kt0 > wq1)) {
         floatx16_t st = zero16();
 #pragma unroll
-        for (int i = 0; i < KS; ++i) st = mfma32(row_frag<D>(sK, 32 * ph, 16 * i, lane), qreg[i], st);
+        for (int i = 0; i < KS; ++i) st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
         const bool diag = a.causal && kt0 + 31 > wq0;
         const bool tail = kt0 + 31 >= S;
         float mx = -INFINITY;
@@ -490,7 +523,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t pb = pack8(st, s2);
 #pragma unroll
-          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<D>(sV, 32 * ph + 16 * s2, d * 32, lane), pb, oacc[d]);
+          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<D>(sV, 32 * ph + 16 * s2, d, fa), pb, oacc[d]);
         }
       }
       wait_vm();
@@ -538,10 +571,11 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
 template <int D>
 __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int nitems) {
   constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
+  __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
   static_assert(6 * DB * 16 * 64 * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int sub = w & 1, ph = w >> 1;
+  const FragAddr<D> fa(lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
   float* cbuf = reinterpret_cast<float*>(smem);
@@ -598,8 +632,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
         floatx16_t st = zero16(), dpt = zero16();
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-          st = mfma32(row_frag<D>(sK, 32 * ph, 16 * i, lane), qreg[i], st);
-          dpt = mfma32(row_frag<D>(sV, 32 * ph, 16 * i, lane), doreg[i], dpt);
+          st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
+          dpt = mfma32(row_frag<D>(sV, 32 * ph, i, fa), doreg[i], dpt);
         }
         const bool diag = a.causal && kt0 + 31 > wq0;
 #pragma unroll
@@ -613,7 +647,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t dsb = pack8(st, s2);
 #pragma unroll
-          for (int d = 0; d < DB; ++d) dqt[d] = mfma32(tr_frag<D>(sK, 32 * ph + 16 * s2, d * 32, lane), dsb, dqt[d]);
+          for (int d = 0; d < DB; ++d) dqt[d] = mfma32(tr_frag<D>(sK, 32 * ph + 16 * s2, d, fa), dsb, dqt[d]);
         }
       }
       wait_vm();
@@ -633,13 +667,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
 template <int D>
 __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, int nitems) {
   constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (Q, dO)
-  __shared__ __attribute__((aligned(16))) bf16_t sVb[64 * D];          // the item's 64 rows of V
+  __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (Q, dO)
+  __shared__ __attribute__((aligned(256))) bf16_t sVb[64 * D];          // the item's 64 rows of V
   __shared__ __attribute__((aligned(16))) float sL[2][kStageRows];
   __shared__ __attribute__((aligned(16))) float sDel[2][kStageRows];
   static_assert(6 * DB * 16 * 64 * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int sub = w & 1, ph = w >> 1;
+  const FragAddr<D> fa(lane);
   const int S = a.S, H = a.H, BH = a.B * a.H;
   const float c = a.scale * kLog2e;
   float* cbuf = reinterpret_cast<float*>(smem);
@@ -703,15 +738,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
         floatx16_t sc = zero16(), dp = zero16();
         // fragments are fetched one k-step ahead; the scheduling barriers keep the compiler from
         // hoisting every LDS read of the stage (which would not fit the register budget)
-        bf16x8_t fq = row_frag<D>(sQ, 32 * ph, 0, lane), fd = row_frag<D>(sdO, 32 * ph, 0, lane),
-                 fv = row_frag<D>(sVb, 32 * sub, 0, lane);
+        bf16x8_t fq = row_frag<D>(sQ, 32 * ph, 0, fa), fd = row_frag<D>(sdO, 32 * ph, 0, fa),
+                 fv = row_frag<D>(sVb, 32 * sub, 0, fa);
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
           bf16x8_t nq = fq, nd = fd, nv = fv;
           if (i + 1 < KS) {
-            nq = row_frag<D>(sQ, 32 * ph, 16 * (i + 1), lane);
-            nd = row_frag<D>(sdO, 32 * ph, 16 * (i + 1), lane);
-            nv = row_frag<D>(sVb, 32 * sub, 16 * (i + 1), lane);
+            nq = row_frag<D>(sQ, 32 * ph, i + 1, fa);
+            nd = row_frag<D>(sdO, 32 * ph, i + 1, fa);
+            nv = row_frag<D>(sVb, 32 * sub, i + 1, fa);
           }
           sc = mfma32(fq, kreg[i], sc);
           dp = mfma32(fd, fv, dp);
@@ -739,13 +774,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t pb = pack8(sc, s2), dsb = pack8(dp, s2);
-          bf16x8_t fo = tr_frag<D>(sdO, 32 * ph + 16 * s2, 0, lane), fq2 = tr_frag<D>(sQ, 32 * ph + 16 * s2, 0, lane);
+          bf16x8_t fo = tr_frag<D>(sdO, 32 * ph + 16 * s2, 0, fa), fq2 = tr_frag<D>(sQ, 32 * ph + 16 * s2, 0, fa);
 #pragma unroll
           for (int d = 0; d < DB; ++d) {
             bf16x8_t no = fo, nq = fq2;
             if (d + 1 < DB) {
-              no = tr_frag<D>(sdO, 32 * ph + 16 * s2, (d + 1) * 32, lane);
-              nq = tr_frag<D>(sQ, 32 * ph + 16 * s2, (d + 1) * 32, lane);
+              no = tr_frag<D>(sdO, 32 * ph + 16 * s2, d + 1, fa);
+              nq = tr_frag<D>(sQ, 32 * ph + 16 * s2, d + 1, fa);
             }
             acc[DB + d] = mfma32(fo, pb, acc[DB + d]);
             acc[d] = mfma32(fq2, dsb, acc[d]);

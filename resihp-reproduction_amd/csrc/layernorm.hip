@@ -196,20 +196,115 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(int64_t rows, int dim, cons
   }
 }
 
-// Column sums of the per-block partial rows: a block owns 64 columns; wave w sums partial
-// rows w, w+4, ... for its lane's column, and the four wave sums are added in wave order
-// (fixed order: deterministic).
+// bf16 rows, dim % 8 == 0: the fast backward.  Lane l owns the 16-byte chunks l + 64c
+// (c < C) of every row.  All loads of a row (dy, x, residual gradient) are issued together and
+// the next row's are in flight while the current one is reduced and written, so each wave
+// keeps ~3*C*16 bytes per lane moving; column partials as in ln_bwd_kernel.
+template <int C>
+__global__ __launch_bounds__(256) void ln_bwd_bf16_kernel(int64_t rows, int dim, const bf16_t* __restrict__ dy,
+                                                           const bf16_t* __restrict__ x, const float* __restrict__ mean,
+                                                           const float* __restrict__ rstd,
+                                                           const bf16_t* __restrict__ gamma,
+                                                           const bf16_t* __restrict__ dres, bf16_t* __restrict__ dx,
+                                                           float* __restrict__ part_g, float* __restrict__ part_b) {
+  __shared__ float red[2][4][64 * 8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const u16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+  bool ok[C];
+  u16x8_t gm[C];
+  float pg[C][8], pb[C][8];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    ok[c] = 8 * (lane + 64 * c) < dim;
+    gm[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(gamma + 8 * (lane + 64 * c)) : z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pg[c][j] = pb[c][j] = 0.f;
+  }
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  auto load = [&](int64_t row, u16x8_t(&a)[C], u16x8_t(&b)[C], u16x8_t(&r)[C]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t off = row * dim + 8 * (lane + 64 * c);
+      a[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(dy + off) : z;
+      b[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(x + off) : z;
+      r[c] = (ok[c] && dres) ? *reinterpret_cast<const u16x8_t*>(dres + off) : z;
+    }
+  };
+  int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  u16x8_t a[C], b[C], r[C];
+  if (row < rows) load(row, a, b, r);
+  for (; row < rows; row += stride) {
+    u16x8_t na[C], nb[C], nr[C];
+    if (row + stride < rows) load(row + stride, na, nb, nr);
+    const float mu = mean[row], rs = rstd[row];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float dv = bf16_to_f32(a[c][j]);
+        const float h = (bf16_to_f32(b[c][j]) - mu) * rs;
+        const float g = dv * bf16_to_f32(gm[c][j]);
+        s1 += g;
+        s2 += g * h;
+        pg[c][j] += dv * h;
+        pb[c][j] += dv;
+      }
+    const float m1 = wave_sum(s1) / (float)dim;
+    const float m2 = wave_sum(s2) / (float)dim;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (!ok[c]) continue;
+      u16x8_t o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float h = (bf16_to_f32(b[c][j]) - mu) * rs;
+        const float g = bf16_to_f32(a[c][j]) * bf16_to_f32(gm[c][j]);
+        o[j] = f32_to_bf16(rs * (g - m1 - h * m2) + bf16_to_f32(r[c][j]));
+      }
+      *reinterpret_cast<u16x8_t*>(dx + row * dim + 8 * (lane + 64 * c)) = o;
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      a[c] = na[c];
+      b[c] = nb[c];
+      r[c] = nr[c];
+    }
+  }
+  // combine the 4 waves' column partials, one chunk of columns at a time (wave order)
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      red[0][wave][lane * 8 + j] = pg[c][j];
+      red[1][wave][lane * 8 + j] = pb[c][j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 8; i += 256) {
+      const int col = 8 * (i / 8 + 64 * c) + i % 8;
+      if (col < dim) {
+        part_g[(int64_t)blockIdx.x * dim + col] = red[0][0][i] + red[0][1][i] + red[0][2][i] + red[0][3][i];
+        part_b[(int64_t)blockIdx.x * dim + col] = red[1][0][i] + red[1][1][i] + red[1][2][i] + red[1][3][i];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Column sums of the per-block partial rows: a block owns 64 columns; its 16 waves sum
+// partial rows w, w+16, ... for their lane's column, and the 16 wave sums are added in wave
+// order (fixed order: deterministic).  16 waves x 32 blocks keep enough loads in flight.
 template <typename T>
-__global__ __launch_bounds__(256) void ln_colsum_kernel(int nblocks, int dim, const float* __restrict__ part_g,
-                                                         const float* __restrict__ part_b, T* dgamma, T* dbeta,
-                                                         int accumulate) {
-  __shared__ float red[2][4][64];
+__global__ __launch_bounds__(1024) void ln_colsum_kernel(int nblocks, int dim, const float* __restrict__ part_g,
+                                                          const float* __restrict__ part_b, T* dgamma, T* dbeta,
+                                                          int accumulate) {
+  __shared__ float red[2][16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
   float sg = 0.f, sb = 0.f;
   if (col < dim) {
 #pragma unroll 8
-    for (int b = wave; b < nblocks; b += 4) {
+    for (int b = wave; b < nblocks; b += 16) {
       sg += part_g[(int64_t)b * dim + col];
       sb += part_b[(int64_t)b * dim + col];
     }
@@ -218,8 +313,13 @@ __global__ __launch_bounds__(256) void ln_colsum_kernel(int nblocks, int dim, co
   red[1][wave][lane] = sb;
   __syncthreads();
   if (wave == 0 && col < dim) {
-    sg = red[0][0][lane] + red[0][1][lane] + red[0][2][lane] + red[0][3][lane];
-    sb = red[1][0][lane] + red[1][1][lane] + red[1][2][lane] + red[1][3][lane];
+    sg = 0.f;
+    sb = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      sg += red[0][w][lane];
+      sb += red[1][w][lane];
+    }
     if (dgamma) st_f32(dgamma + col, accumulate ? ld_f32(dgamma + col) + sg : sg);
     if (dbeta) st_f32(dbeta + col, accumulate ? ld_f32(dbeta + col) + sb : sb);
   }
@@ -273,6 +373,19 @@ struct BwdLauncher {
     return rh_check_launch("rh_layernorm_bwd");
   }
 };
+
+int launch_bwd_bf16(int64_t rows, int dim, const void* dy, const void* x, const float* mean, const float* rstd,
+                    const void* gamma, const void* dres, void* dx, float* pg, float* pb, int nb, hipStream_t st) {
+  const int chunks = (dim + 511) / 512;
+#define RH_LN_BWD(CC)                                                                                              \
+  hipLaunchKernelGGL((ln_bwd_bf16_kernel<CC>), dim3((unsigned)nb), dim3(256), 0, st, rows, dim, (const bf16_t*)dy, \
+                     (const bf16_t*)x, mean, rstd, (const bf16_t*)gamma, (const bf16_t*)dres, (bf16_t*)dx, pg, pb)
+  if (chunks <= 1) RH_LN_BWD(1);
+  else if (chunks <= 2) RH_LN_BWD(2);
+  else RH_LN_BWD(4);
+#undef RH_LN_BWD
+  return rh_check_launch("rh_layernorm_bwd");
+}
 
 int check_ln(int dtype, int64_t rows, int64_t dim) {
   RH_REQUIRE(dtype == RH_DTYPE_F32 || dtype == RH_DTYPE_BF16, "rh_layernorm: unknown dtype %d", dtype);
@@ -329,7 +442,9 @@ extern "C" int rh_layernorm_bwd(int dtype, int64_t rows, int64_t dim, const void
   float* pb = pg + (int64_t)nb * dim;
   const bool vec = dim % 8 == 0 && rh_aligned(dy, 16) && rh_aligned(x, 16) && rh_aligned(dx, 16) &&
                    rh_aligned(gamma, 16) && (dresidual == nullptr || rh_aligned(dresidual, 16));
-  if (dtype == RH_DTYPE_BF16)
+  if (dtype == RH_DTYPE_BF16 && vec && dim <= 2048)
+    rc = launch_bwd_bf16(rows, (int)dim, dy, x, mean, rstd, gamma, dresidual, dx, pg, pb, nb, st);
+  else if (dtype == RH_DTYPE_BF16)
     rc = dispatch_ln<bf16_t, BwdLauncher>((int)dim, vec, rows, (int)dim, dy, x, mean, rstd, gamma, dresidual, dx, pg,
                                           pb, nb, st);
   else
@@ -339,10 +454,10 @@ extern "C" int rh_layernorm_bwd(int dtype, int64_t rows, int64_t dim, const void
   if (dgamma || dbeta) {
     const unsigned blocks = (unsigned)rh_cdiv(dim, 64);
     if (dtype == RH_DTYPE_BF16)
-      hipLaunchKernelGGL(ln_colsum_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, nb, (int)dim, pg, pb,
+      hipLaunchKernelGGL(ln_colsum_kernel<bf16_t>, dim3(blocks), dim3(1024), 0, st, nb, (int)dim, pg, pb,
                          (bf16_t*)dgamma, (bf16_t*)dbeta, accumulate);
     else
-      hipLaunchKernelGGL(ln_colsum_kernel<float>, dim3(blocks), dim3(256), 0, st, nb, (int)dim, pg, pb,
+      hipLaunchKernelGGL(ln_colsum_kernel<float>, dim3(blocks), dim3(1024), 0, st, nb, (int)dim, pg, pb,
                          (float*)dgamma, (float*)dbeta, accumulate);
     return rh_check_launch("rh_layernorm_bwd colsum");
   }
