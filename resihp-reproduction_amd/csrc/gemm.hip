@@ -1,20 +1,26 @@
 // Dense GEMMs of the decoder block (F.linear and its backward) for gfx950.
 //
 // bf16 path (MFMA).  Workgroup tiles of BM x BN x 64 built from
-// v_mfma_f32_32x32x16_bf16 (the 32x32 form: ~2.2 PFLOP/s sustained on MI355X,
-// the 16x16x32 form reaches barely half that).  Three tile shapes:
+// v_mfma_f32_32x32x16_bf16 (measured on MI355X: ~2.1 PFLOP/s sustained for both the
+// 32x32x16 and 16x16x32 forms; the 32x32 form needs half the operand reads).  Three tile
+// shapes:
 //   256x256, 8 waves (2x4, 128x64 per wave)   -- large outputs
 //   256x128, 8 waves (4x2,  64x64 per wave)   -- medium
 //   128x128, 4 waves (2x2,  64x64 per wave)   -- small / split-K
 // chosen per call by the number of tiles against the CU count.
 //
-// Operands are staged through LDS, double-buffered (global loads of k-tile
-// t+1 are in flight while the MFMAs of tile t run; one barrier per k-tile):
+// Two main loops share the LDS layouts, fragment reads and epilogue:
+//   gemm_bf16_dma  -- operands go global->LDS with direct-to-LDS loads (the default
+//                     whenever the operands can be addressed without bounds checks);
+//   gemm_bf16_mfma -- operands staged through registers with bounds checks (ragged
+//                     edges, K not a multiple of 64, unaligned rows).
+// Both double-buffer the LDS tiles (loads of k-tile t+1 in flight while the MFMAs of
+// tile t run; one barrier per k-tile):
 //   k-contiguous operand  (A of NT/NN, B of NT): LDS [rows][64], 128-byte rows,
 //     16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7), so the 16
 //     rows a ds_read_b128 phase touches hit 16 distinct bank groups;
 //   m/n-contiguous operand (A of TN, B of NN/TN): LDS [64][cols] exactly as in
-//     memory (16-byte stores), 32-element unit u of row k stored at u ^ (k & 3),
+//     memory, 32-element unit u of row k stored at u ^ (k & 3),
 //     and MFMA fragments are read with ds_read_b64_tr_b16: in each 16-lane
 //     block, lane i addresses row k0 + i/4, columns c0 + 4*(i%4) .. +3, and lane
 //     j receives rows k0..k0+3 of column c0 + j -- a k-major fragment without
@@ -465,43 +471,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16
 
 
 // ---------------------------------------------------------------------------
-// bf16 MFMA kernel, pipelined: NST-stage LDS ring fed by direct global->LDS loads
+// bf16 MFMA kernel fed by direct global->LDS loads
 // ---------------------------------------------------------------------------
-// k-tile 32, NST = 5 stages for 256x256 tiles (160 KB).  Iteration t issues the loads of tile
-// t+NST-1 (global_load_lds_dwordx4: no staging registers, no LDS write instructions), runs the
-// two k-steps of tile t from registers while reading the next fragments, and reads tile t+1's
-// first fragments before the barrier that ends the iteration -- so the MFMA pipe has work
-// queued across every barrier.  The barrier publishes tile t+2 (each thread first waits for its
-// own loads of that tile, leaving up to NST-3 younger tiles in flight: the loads are
-// latency-bound, so depth is throughput) and frees stage t for tile t+NST.  Needs: bf16, 16-byte aligned rows, K per split a multiple of 32, m/n-
-// contiguous operand extents a multiple of 8, segment boundaries a multiple of 32 k-rows.
-// Rows / columns past the matrix edge are clamped onto the last valid ones (their results
-// are never stored).
-constexpr int dBK = 32;
-
-// LDS ring depth per tile shape: as many 32-deep stages as the LDS budget holds (at most 6);
-// 128x128 tiles keep to 80 KB so that two workgroups share a CU
-template <int BM, int BN>
-constexpr int dma_stages() {
-  constexpr int budget = (BM == 128 && BN == 128) ? 80 * 1024 : 160 * 1024;
-  constexpr int n = budget / ((BM + BN) * dBK * 2);
-  return n > 6 ? 6 : n;
-}
-
 typedef __attribute__((address_space(3))) void lds_void_t;
-
-// element offset of (row r, 16-byte chunk c) in a k-contiguous [R][32] tile: 64-byte rows,
-// chunk c stored at c ^ ((r >> 2) & 3), so 16 consecutive rows hit 16 distinct bank groups
-__device__ __forceinline__ int kc32_off(int r, int c) { return r * dBK + ((c ^ ((r >> 2) & 3)) << 3); }
-
-template <int ROWS, bool KC>
-__device__ __forceinline__ bf16x8_t load_frag32(const bf16_t* s, int rb, int ks, int lane) {
-  if (KC) {
-    const int r = rb + (lane & 31);
-    return *reinterpret_cast<const bf16x8_t*>(s + kc32_off(r, ks * 2 + (lane >> 5)));
-  }
-  return load_frag<ROWS, false>(s, rb, ks, lane);
-}
 
 // Direct global->LDS load of 16 bytes per lane: lane l of the wave writes LDS bytes
 // lds_base + 16*l .. +15 (lds_base wave-uniform).  Issued through inline asm on purpose: the
@@ -520,16 +492,29 @@ __device__ __forceinline__ void dma16(const bf16_t* src, const bf16_t* lds_dst) 
       : "memory", "m0");
 }
 
-// One operand's share of a k-tile, issued as 1 KB direct-to-LDS windows (lane l of a window
-// lands at window byte 16*l).  KC: window = 16 rows x 4 chunks; !KC: window = 512/ROWS k-rows.
+// wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
+// outstanding; they complete in issue order
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+// The operand tiles go global->LDS with global_load_lds_dwordx4 (no staging registers, no LDS
+// write instructions).  k-tiles are 64 deep so that every k-contiguous row piece a load fetches
+// is a whole 128-byte cache line (measured on MI355X: the L2->CU path delivers ~1.5-2x more
+// bytes per clock for whole lines than for 64-byte halves).  Two stages (128 KB at 256x256):
+// tile t+1 is loaded while tile t is computed; each k-step's fragments are read during the
+// previous k-step's MFMAs.  LDS layouts are the register-staged kernel's (kc_off / mc_off).
+// Needs: 16-byte aligned rows, K and the K per split multiples of 64, m/n-contiguous operand
+// extents multiples of 8, B segment boundaries multiples of 64 k-rows.  Rows / columns past
+// the matrix edge are clamped onto the last valid ones (their results are never stored).
 template <int ROWS, bool KC, int NWAVES>
 struct DmaOperand {
-  static constexpr int WIN = ROWS * dBK * 2 / 1024;
+  static constexpr int WIN = ROWS * kBK * 2 / 1024;
   static constexpr int PER = WIN / NWAVES;
   static_assert(WIN % NWAVES == 0, "tile windows must split evenly over the waves");
   static constexpr int KROWS = 512 / ROWS;  // !KC: k-rows per window
-  // KC: per-lane row pointers (advanced by dBK per tile); !KC: per-lane element offset from the
-  // k-tile's first row (k-row within the tile * ld + column)
   const bf16_t* rowp[PER];
   int64_t off[PER];
 
@@ -540,37 +525,27 @@ struct DmaOperand {
     for (int i = 0; i < PER; ++i) {
       const int win = wave + NWAVES * i;
       if (KC) {
-        const int row = win * 16 + lane / 4;
-        const int lchunk = (lane & 3) ^ ((row >> 2) & 3);
+        const int row = win * 8 + lane / 8;
+        const int lchunk = (lane & 7) ^ ((row >> 1) & 7);  // inverse of kc_off's chunk swizzle
         const int64_t gr = min(o0 + row, extent - 1);
         rowp[i] = rowptr(gr) + kbeg + lchunk * 8;
       } else {
         const int kr = win * KROWS + lane / (ROWS / 8);
         const int pchunk = lane % (ROWS / 8);
-        const int lunit = (pchunk >> 2) ^ (kr & 3);
+        const int lunit = (pchunk >> 2) ^ (kr & 3);  // inverse of mc_off's unit swizzle
         const int64_t c = o0 + lunit * 32 + (pchunk & 3) * 8;
         off[i] = (int64_t)kr * ld + min(c, extent - 8);
       }
     }
   }
-
-  // issue tile kt into LDS tile `dst`; `krow0` = pointer to the tile's first k-row (!KC)
   __device__ __forceinline__ void issue(bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int win = wave + NWAVES * i;
-      dma16(KC ? rowp[i] + (int64_t)kt * dBK : krow0 + off[i], dst + win * 512);
+      dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + win * 512);
     }
   }
 };
-
-// wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
-// outstanding; they complete in issue order
-template <int N>
-__device__ __forceinline__ void wait_vm_le() {
-  static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
-}
 
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_t> p) {
@@ -578,20 +553,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
   constexpr bool A_KC = (L != RH_GEMM_TN);
   constexpr bool B_KC = (L == RH_GEMM_NT);
   constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
-  constexpr int A_ELEMS = BM * dBK, B_ELEMS = BN * dBK, STAGE = A_ELEMS + B_ELEMS;
-  constexpr int NST = dma_stages<BM, BN>();
-  static_assert(NST >= 4, "the pipeline needs at least four stages");
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK, STAGE = A_ELEMS + B_ELEMS;
   using DA = DmaOperand<BM, A_KC, NW>;
   using DB = DmaOperand<BN, B_KC, NW>;
-  constexpr int PT = DA::PER + DB::PER;  // loads per thread per k-tile
-  __shared__ __attribute__((aligned(16))) bf16_t smem[NST * STAGE];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
 
   int tm, tn;
   tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t kbeg = (int64_t)blockIdx.z * p.k_per_split;
   const int64_t kend = min(p.K, kbeg + p.k_per_split);
-  const int nk = (int)((kend - kbeg) / dBK);
+  const int nk = (int)((kend - kbeg) / kBK);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
 
@@ -599,32 +571,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
   DB db;
   da.setup([&](int64_t r) { return p.A + r * p.lda; }, m0, p.M, kbeg, p.lda, wave, lane);
   db.setup([&](int64_t r) { return b_row(p, r); }, n0, p.N, kbeg, p.ldb, wave, lane);
-  // B segments of an m/n-contiguous B (k-rows split over up to RH_MAX_SEG tensors): a k-tile
-  // never straddles one, so the issuing side tracks (segment, row in segment) as it advances --
-  // no division and no kernel-argument load inside the loop.
-  // (All of it uniform, kept in scalar registers: 32-bit row counters, a select chain rather
-  // than an indexed array.)
   const bf16_t* const bs0 = p.B[0];
   const bf16_t* const bs1 = p.B[1 % RH_MAX_SEG];
   const bf16_t* const bs2 = p.B[2 % RH_MAX_SEG];
   const bf16_t* const bs3 = p.B[3 % RH_MAX_SEG];
-  static_assert(RH_MAX_SEG == 4, "segment select assumes four B pointers");
   const int bseg_rows = (!B_KC && p.b_nseg > 1) ? (int)p.b_seg : INT32_MAX;
-  int iss_seg = 0, iss_row = (int)kbeg;  // segment and row-in-segment of the next tile to issue
+  int iss_seg = 0, iss_row = (int)kbeg;
   if (!B_KC && p.b_nseg > 1) {
     iss_seg = (int)kbeg / bseg_rows;
     iss_row = (int)kbeg - iss_seg * bseg_rows;
   }
   auto issue = [&](int kt) {
-    bf16_t* st = smem + (kt % NST) * STAGE;
-    const int64_t k0 = kbeg + (int64_t)kt * dBK;
+    bf16_t* st = smem + (kt & 1) * STAGE;
+    const int64_t k0 = kbeg + (int64_t)kt * kBK;
     da.issue(st, kt, A_KC ? nullptr : p.A + k0 * p.lda, wave);
     if (B_KC) {
       db.issue(st + A_ELEMS, kt, nullptr, wave);
     } else {
       const bf16_t* base = iss_seg == 0 ? bs0 : iss_seg == 1 ? bs1 : iss_seg == 2 ? bs2 : bs3;
       db.issue(st + A_ELEMS, kt, base + (int64_t)iss_row * p.ldb, wave);
-      iss_row += dBK;
+      iss_row += kBK;
       if (iss_row >= bseg_rows) {
         iss_row -= bseg_rows;
         ++iss_seg;
@@ -640,65 +606,44 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  bf16x8_t fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-  auto read_frags = [&](bf16x8_t(&fa)[FM], bf16x8_t(&fb)[FN], int kt, int ks) {
-    const bf16_t* st = smem + (kt % NST) * STAGE;
+  bf16x8_t fa[2][FM], fb[2][FN];
+  auto read_frags = [&](int set, const bf16_t* st, int ks) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[i] = load_frag32<BM, A_KC>(st, wm * WTM + i * 32, ks, lane);
+    for (int i = 0; i < FM; ++i) fa[set][i] = load_frag<BM, A_KC>(st, wm * WTM + i * 32, ks, lane);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[j] = load_frag32<BN, B_KC>(st + A_ELEMS, wn * WTN + j * 32, ks, lane);
+    for (int j = 0; j < FN; ++j) fb[set][j] = load_frag<BN, B_KC>(st + A_ELEMS, wn * WTN + j * 32, ks, lane);
   };
-  auto mma = [&](const bf16x8_t(&fa)[FM], const bf16x8_t(&fb)[FN]) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-  };
-
-  // wait until tile `need` has landed, given that tiles up to `issued` have been issued
-  auto wait_tile = [&](int need, int issued) {
-    const int younger = issued - need;  // tiles allowed in flight
-    if (younger >= 3) wait_vm_le<3 * PT>();
-    else if (younger == 2) wait_vm_le<2 * PT>();
-    else if (younger == 1) wait_vm_le<PT>();
-    else wait_vm_le<0>();
-  };
-  if (nk > 0) {
-    const int pro = min(nk, NST - 1);
-    for (int t = 0; t < pro; ++t) issue(t);
-    // iteration 0 reads tiles 0 and 1
-    wait_tile(min(1, nk - 1), pro - 1);
-    __syncthreads();
-    read_frags(fa0, fb0, 0, 0);
-  }
-  // LDS instructions per fragment set (a transposed fragment takes two reads)
   constexpr int NREAD = FM * (A_KC ? 1 : 2) + FN * (B_KC ? 1 : 2);
+
+  if (nk > 0) {
+    issue(0);
+    wait_vm_le<0>();
+    __syncthreads();
+  }
 #pragma unroll 1
   for (int kt = 0; kt < nk; ++kt) {
-    const int nxt = kt + NST - 1;
-    if (nxt < nk) issue(nxt);
-    // every read of the next fragment set is issued before the MFMAs on the current one, so
-    // the LDS latency hides behind FM*FN MFMAs (the scheduler would otherwise recycle the
-    // current set's registers and serialise them)
-    read_frags(fa1, fb1, kt, 1);
-    mma(fa0, fb0);
-    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // unconditional (the last iteration reads a stale stage it never uses): a branch here would
-    // make the wait-count pass merge both paths and over-wait on the next tile's reads
-    read_frags(fa0, fb0, kt + 1, 0);
-    mma(fa1, fb1);
-    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // tile kt+2 must have landed before the barrier publishes it; younger tiles may still fly
-    wait_tile(min(kt + 2, nk - 1), min(nxt, nk - 1));
+    if (kt + 1 < nk) issue(kt + 1);
+    const bf16_t* st = smem + (kt & 1) * STAGE;
+    read_frags(0, st, 0);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      if (ks + 1 < kBK / 16) read_frags((ks + 1) & 1, st, ks + 1);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
+      if (ks + 1 < kBK / 16) {
+        __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vm_le<0>();  // tile kt+1 has landed
     __syncthreads();
   }
 
-  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, NST * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -982,20 +927,18 @@ void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipSt
   }
 }
 
-// The pipelined direct-to-LDS kernel covers every call whose operands it can address without
-// bounds checks (see gemm_bf16_dma); RESIHP_GEMM_DMA=0 forces the register-staged kernel.
+// The direct-to-LDS kernel covers every call whose operands it can address without bounds
+// checks (see gemm_bf16_dma); RESIHP_GEMM_DMA=0 forces the register-staged kernel.
 bool dma_ok(const rh_gemm_desc* d, const Plan& pl, const GemmParams<bf16_t>& p) {
   static const int enabled = [] {
     const char* e = getenv("RESIHP_GEMM_DMA");
     return (e && e[0] == '0' && e[1] == 0) ? 0 : 1;
   }();
-  if (!enabled || !p.aligned || d->K % dBK || pl.k_per_split % dBK) return false;
-  // measured on MI355X: faster for NT and NN, slower than the register-staged kernel for TN
-  if (d->layout == RH_GEMM_TN) return false;
+  if (!enabled || !p.aligned || d->K % kBK || pl.k_per_split % kBK) return false;
   const bool a_kc = d->layout != RH_GEMM_TN, b_kc = d->layout == RH_GEMM_NT;
   if (!a_kc && (d->M < 8 || d->M % 8)) return false;
   if (!b_kc && (d->N < 8 || d->N % 8)) return false;
-  if (!b_kc && d->b_nseg > 1 && d->b_seg_rows % dBK) return false;
+  if (!b_kc && d->b_nseg > 1 && d->b_seg_rows % kBK) return false;
   return true;
 }
 
