@@ -61,6 +61,12 @@ const char* rh_last_error(void);
  *                                                       model.py:81, tp.py:247)
  *   RH_EPI_GELU_GRAD D = v * gelu'(aux)                  (GELU backward fused
  *                                                       into the fc2 dgrad)
+ *   RH_EPI_GELU_DERIV aux_out = gelu'(v), D = gelu(v)    (fc1 forward keeping the
+ *                                                       derivative for backward)
+ *   RH_EPI_MUL_AUX   D = v * aux                         (fc2 dgrad times the kept
+ *                                                       derivative)
+ * bf16 results evaluate gelu / gelu' with Abramowitz & Stegun 7.1.26 for the normal
+ * CDF (|error| <= 7e-8, far below bf16 resolution); fp32 results use erff/expf.
  * Segmented operands let three separate q/k/v weights act as one [3*d_l, d]
  * matrix without a copy: row r of the *stored* B lives at
  * B[r / b_seg_rows] + (r % b_seg_rows)*ldb, and row m of D lives at
@@ -75,6 +81,8 @@ const char* rh_last_error(void);
 #define RH_EPI_NONE 0
 #define RH_EPI_GELU 1
 #define RH_EPI_GELU_GRAD 2
+#define RH_EPI_GELU_DERIV 3
+#define RH_EPI_MUL_AUX 4
 
 #define RH_MAX_SEG 4
 

@@ -1,7 +1,7 @@
 // Shared device/host helpers for the resihp HIP library (gfx950 / CDNA4).
 //
 // Storage types: fp32 (`float`) and bf16 (raw `uint16_t`, round-to-nearest-even
-// on store, identical to torch's float->bfloat16 conversion). Every kernel
+// on store, identical to torch's float->bfloat16 conversion for non-NaN values). Every kernel
 // accumulates in fp32.
 #pragma once
 
@@ -32,13 +32,9 @@ __device__ __host__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return f;
 }
 
-__device__ __host__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u;
-  __builtin_memcpy(&u, &f, 4);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)0x7fc0;  // NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// Round to nearest even with gfx950's v_cvt_pk_bf16_f32: the same bits as torch's
+// float->bfloat16 conversion for every non-NaN value (NaNs stay NaNs).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
 template <typename T> struct Storage;
 template <> struct Storage<float> {
@@ -67,6 +63,33 @@ __device__ __forceinline__ float gelu_grad_f(float x) {
   const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
   const float pdf = expf(-0.5f * x * x) * 0.39894228040143267794f;
   return cdf + x * pdf;
+}
+
+// GELU for results that are rounded to bf16 (the bf16 GEMM epilogues and elementwise
+// kernels).  The normal CDF uses Abramowitz & Stegun, Handbook of Mathematical Functions
+// (1964), formula 7.1.26: for z >= 0, erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5)
+// exp(-z^2) with t = 1/(1 + p z), |error| <= 1.5e-7 -- three orders of magnitude below bf16
+// resolution.  With z = |x|/sqrt(2), exp(-z^2) = exp(-x^2/2) is also the Gaussian density's
+// factor, so the value and the derivative share one exp and one reciprocal (hardware
+// v_exp_f32 / v_rcp_f32) instead of an erf and an exp each.
+struct GeluParts {
+  float cdf;  // Phi(x)
+  float pdf;  // phi(x)
+};
+__device__ __forceinline__ GeluParts gelu_parts_fast(float x) {
+  constexpr float kP = 0.3275911f, kA1 = 0.254829592f, kA2 = -0.284496736f, kA3 = 1.421413741f,
+                  kA4 = -1.453152027f, kA5 = 1.061405429f;
+  const float ax = fabsf(x);
+  const float e = __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634074f));  // exp(-x^2/2)
+  const float t = __builtin_amdgcn_rcpf(fmaf(kP * 0.70710678118654752440f, ax, 1.0f));
+  const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, kA5, kA4), kA3), kA2), kA1);
+  const float tail = 0.5f * poly * e;  // = Phi(-|x|)
+  return {x >= 0.f ? 1.0f - tail : tail, e * 0.39894228040143267794f};
+}
+__device__ __forceinline__ float gelu_fast_f(float x) { return x * gelu_parts_fast(x).cdf; }
+__device__ __forceinline__ float gelu_grad_fast_f(float x) {
+  const GeluParts g = gelu_parts_fast(x);
+  return g.cdf + x * g.pdf;
 }
 
 // ---------------------------------------------------------------------------

@@ -17,13 +17,13 @@ unsigned grid_for(int64_t n) {
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gelu_fwd_kernel(int64_t n, const T* x, T* y) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
-    st_f32(y + i, gelu_f(ld_f32(x + i)));
+    st_f32(y + i, std::is_same<T, bf16_t>::value ? gelu_fast_f(ld_f32(x + i)) : gelu_f(ld_f32(x + i)));
 }
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(int64_t n, const T* x, const T* dy, T* dx) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
-    st_f32(dx + i, ld_f32(dy + i) * gelu_grad_f(ld_f32(x + i)));
+    st_f32(dx + i, ld_f32(dy + i) * (std::is_same<T, bf16_t>::value ? gelu_grad_fast_f(ld_f32(x + i)) : gelu_grad_f(ld_f32(x + i))));
 }
 
 template <typename T>

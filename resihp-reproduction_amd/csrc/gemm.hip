@@ -96,14 +96,46 @@ __device__ __forceinline__ void epilogue_store(const GemmParams<T>& p, int64_t m
     const T* c = p.C ? (p.C + m * p.ldc + n) : (drow + n);
     v += p.beta * ld_f32(c);
   }
+  constexpr bool kBf16 = std::is_same<T, bf16_t>::value;  // bf16 results: fast GELU (see common.hpp)
   if (EPI == RH_EPI_GELU) {
     st_f32(p.aux_out + m * p.ldaux + n, v);
-    v = gelu_f(v);
+    v = kBf16 ? gelu_fast_f(v) : gelu_f(v);
+  } else if (EPI == RH_EPI_GELU_DERIV) {
+    st_f32(p.aux_out + m * p.ldaux + n, kBf16 ? gelu_grad_fast_f(v) : gelu_grad_f(v));
+    v = kBf16 ? gelu_fast_f(v) : gelu_f(v);
   } else if (EPI == RH_EPI_GELU_GRAD) {
-    v *= gelu_grad_f(ld_f32(p.aux + m * p.ldaux + n));
+    const float a = ld_f32(p.aux + m * p.ldaux + n);
+    v *= kBf16 ? gelu_grad_fast_f(a) : gelu_grad_f(a);
+  } else if (EPI == RH_EPI_MUL_AUX) {
+    v *= ld_f32(p.aux + m * p.ldaux + n);
   }
   st_f32(drow + n, v);
 }
+
+// The epilogue on 8 consecutive outputs of one row (bf16 storage): aux read/write and the
+// GELU forms.  `xp` is the aux row pointer for this chunk (aux_out or aux by epilogue).
+template <int EPI>
+__device__ __forceinline__ void epi8_bf16(float (&v)[8], bf16_t* xp) {
+  if (EPI == RH_EPI_GELU || EPI == RH_EPI_GELU_DERIV) {
+    u16x8_t o;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const GeluParts g = gelu_parts_fast(v[t]);
+      o[t] = f32_to_bf16(EPI == RH_EPI_GELU ? v[t] : g.cdf + v[t] * g.pdf);
+      v[t] *= g.cdf;
+    }
+    *reinterpret_cast<u16x8_t*>(xp) = o;
+  } else if (EPI == RH_EPI_GELU_GRAD || EPI == RH_EPI_MUL_AUX) {
+    const u16x8_t a = *reinterpret_cast<const u16x8_t*>(xp);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] *= EPI == RH_EPI_GELU_GRAD ? gelu_grad_fast_f(bf16_to_f32(a[t])) : bf16_to_f32(a[t]);
+  }
+}
+
+template <int EPI>
+constexpr bool epi_writes_aux() { return EPI == RH_EPI_GELU || EPI == RH_EPI_GELU_DERIV; }
+template <int EPI>
+constexpr bool epi_reads_aux() { return EPI == RH_EPI_GELU_GRAD || EPI == RH_EPI_MUL_AUX; }
 
 // XCD-aware, GROUP_M-grouped tile coordinates of this workgroup.
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
@@ -334,8 +366,8 @@ __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, 
       }
       bf16_t* dp = d_row(p, m) + n;
       const bf16_t* cp = p.C ? p.C + m * p.ldc + n : dp;
-      const bf16_t* xp = EPI == RH_EPI_GELU ? p.aux_out + m * p.ldaux + n
-                                            : (EPI == RH_EPI_GELU_GRAD ? p.aux + m * p.ldaux + n : dp);
+      const bf16_t* xp = epi_writes_aux<EPI>() ? p.aux_out + m * p.ldaux + n
+                                                : (epi_reads_aux<EPI>() ? p.aux + m * p.ldaux + n : dp);
       const bool vec = n + 8 <= p.N && (((uintptr_t)dp | (uintptr_t)xp) & 15) == 0 &&
                        (p.beta == 0.f || ((uintptr_t)cp & 15) == 0);
       if (vec) {
@@ -347,18 +379,8 @@ __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, 
 #pragma unroll
           for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
         }
+        epi8_bf16<EPI>(v, const_cast<bf16_t*>(xp));
         u16x8_t o;
-        if (EPI == RH_EPI_GELU) {
-#pragma unroll
-          for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
-          *reinterpret_cast<u16x8_t*>(const_cast<bf16_t*>(xp)) = o;
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
-        } else if (EPI == RH_EPI_GELU_GRAD) {
-          const u16x8_t a = *reinterpret_cast<const u16x8_t*>(xp);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
-        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
         *reinterpret_cast<u16x8_t*>(dp) = o;
@@ -751,18 +773,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_vec(GemmParams<bf16_t>
 #pragma unroll
       for (int t = 0; t < 8; ++t) v[t] *= p.alpha;
     }
+    epi8_bf16<EPI>(v, epi_writes_aux<EPI>() ? p.aux_out + m * p.ldaux + n
+                                            : const_cast<bf16_t*>(epi_reads_aux<EPI>() ? p.aux + m * p.ldaux + n : dp));
     u16x8_t o;
-    if (EPI == RH_EPI_GELU) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
-      *reinterpret_cast<u16x8_t*>(p.aux_out + m * p.ldaux + n) = o;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = gelu_f(v[t]);
-    } else if (EPI == RH_EPI_GELU_GRAD) {
-      const u16x8_t a = *reinterpret_cast<const u16x8_t*>(p.aux + m * p.ldaux + n);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] *= gelu_grad_f(bf16_to_f32(a[t]));
-    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) o[t] = f32_to_bf16(v[t]);
     *reinterpret_cast<u16x8_t*>(dp) = o;
@@ -841,7 +854,7 @@ int validate(const rh_gemm_desc* d) {
   RH_REQUIRE(d != nullptr, "rh_gemm: null descriptor");
   RH_REQUIRE(d->dtype == RH_DTYPE_F32 || d->dtype == RH_DTYPE_BF16, "rh_gemm: unknown dtype %d", d->dtype);
   RH_REQUIRE(d->layout >= RH_GEMM_NT && d->layout <= RH_GEMM_TN, "rh_gemm: unknown layout %d", d->layout);
-  RH_REQUIRE(d->epilogue >= RH_EPI_NONE && d->epilogue <= RH_EPI_GELU_GRAD, "rh_gemm: unknown epilogue %d",
+  RH_REQUIRE(d->epilogue >= RH_EPI_NONE && d->epilogue <= RH_EPI_MUL_AUX, "rh_gemm: unknown epilogue %d",
              d->epilogue);
   RH_REQUIRE(d->M >= 0 && d->N >= 0 && d->K >= 0, "rh_gemm: negative extent M=%lld N=%lld K=%lld",
              (long long)d->M, (long long)d->N, (long long)d->K);
@@ -874,8 +887,10 @@ int validate(const rh_gemm_desc* d) {
   if (d->beta != 0.f && d->C) RH_REQUIRE(d->ldc >= d->N, "rh_gemm: ldc %lld < N", (long long)d->ldc);
   if (d->epilogue != RH_EPI_NONE) {
     RH_REQUIRE(d->ldaux >= d->N, "rh_gemm: ldaux %lld < N", (long long)d->ldaux);
-    if (d->epilogue == RH_EPI_GELU) RH_REQUIRE(d->aux_out, "rh_gemm: GELU epilogue needs aux_out");
-    if (d->epilogue == RH_EPI_GELU_GRAD) RH_REQUIRE(d->aux, "rh_gemm: GELU_GRAD epilogue needs aux");
+    if (d->epilogue == RH_EPI_GELU || d->epilogue == RH_EPI_GELU_DERIV)
+      RH_REQUIRE(d->aux_out, "rh_gemm: epilogue %d needs aux_out", d->epilogue);
+    if (d->epilogue == RH_EPI_GELU_GRAD || d->epilogue == RH_EPI_MUL_AUX)
+      RH_REQUIRE(d->aux, "rh_gemm: epilogue %d needs aux", d->epilogue);
   }
   return RH_OK;
 }
@@ -970,8 +985,10 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
       bool vec = d->N % 8 == 0 && d->ldd % 8 == 0 && rh_aligned(ws, 16);
       for (int q = 0; q < d->d_nseg; ++q) vec = vec && rh_aligned(d->D[q], 16);
       if (d->beta != 0.f && d->C) vec = vec && rh_aligned(d->C, 16) && d->ldc % 8 == 0;
-      if (d->epilogue != RH_EPI_NONE)
-        vec = vec && rh_aligned(d->epilogue == RH_EPI_GELU ? d->aux_out : d->aux, 16) && d->ldaux % 8 == 0;
+      if (d->epilogue != RH_EPI_NONE) {
+        const bool writes = d->epilogue == RH_EPI_GELU || d->epilogue == RH_EPI_GELU_DERIV;
+        vec = vec && rh_aligned(writes ? d->aux_out : d->aux, 16) && d->ldaux % 8 == 0;
+      }
       if (vec) {
         int64_t blocks = rh_cdiv(total / 8, 256);
         if (blocks > 8 * 1024) blocks = 8 * 1024;
@@ -1002,7 +1019,9 @@ int launch_dtype(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st
   switch (d->epilogue) {
     case RH_EPI_NONE: return launch_epi<T, RH_EPI_NONE>(d, pl, ws, st);
     case RH_EPI_GELU: return launch_epi<T, RH_EPI_GELU>(d, pl, ws, st);
-    default: return launch_epi<T, RH_EPI_GELU_GRAD>(d, pl, ws, st);
+    case RH_EPI_GELU_GRAD: return launch_epi<T, RH_EPI_GELU_GRAD>(d, pl, ws, st);
+    case RH_EPI_GELU_DERIV: return launch_epi<T, RH_EPI_GELU_DERIV>(d, pl, ws, st);
+    default: return launch_epi<T, RH_EPI_MUL_AUX>(d, pl, ws, st);
   }
 }
 
@@ -1038,7 +1057,11 @@ extern "C" int rh_gemm(const rh_gemm_desc* desc, void* workspace, int64_t worksp
     switch (desc->epilogue) {
       case RH_EPI_NONE: return bf16 ? launch_k0<bf16_t, RH_EPI_NONE>(desc, st) : launch_k0<float, RH_EPI_NONE>(desc, st);
       case RH_EPI_GELU: return bf16 ? launch_k0<bf16_t, RH_EPI_GELU>(desc, st) : launch_k0<float, RH_EPI_GELU>(desc, st);
-      default: return bf16 ? launch_k0<bf16_t, RH_EPI_GELU_GRAD>(desc, st) : launch_k0<float, RH_EPI_GELU_GRAD>(desc, st);
+      case RH_EPI_GELU_GRAD:
+        return bf16 ? launch_k0<bf16_t, RH_EPI_GELU_GRAD>(desc, st) : launch_k0<float, RH_EPI_GELU_GRAD>(desc, st);
+      case RH_EPI_GELU_DERIV:
+        return bf16 ? launch_k0<bf16_t, RH_EPI_GELU_DERIV>(desc, st) : launch_k0<float, RH_EPI_GELU_DERIV>(desc, st);
+      default: return bf16 ? launch_k0<bf16_t, RH_EPI_MUL_AUX>(desc, st) : launch_k0<float, RH_EPI_MUL_AUX>(desc, st);
     }
   }
   Plan pl = plan_gemm(desc);

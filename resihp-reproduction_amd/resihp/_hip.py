@@ -31,6 +31,8 @@ RH_GEMM_TN = 2
 RH_EPI_NONE = 0
 RH_EPI_GELU = 1
 RH_EPI_GELU_GRAD = 2
+RH_EPI_GELU_DERIV = 3
+RH_EPI_MUL_AUX = 4
 
 RH_MAX_SEG = 4
 

@@ -130,8 +130,9 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
 
 
 def linear_fwd(x2: torch.Tensor, ws: list, *, residual: torch.Tensor | None = None,
-               gelu_pre: torch.Tensor | None = None) -> torch.Tensor:
-    """y = x . W^T for W = cat(ws, 0) (+ residual); GELU epilogue when gelu_pre is given."""
+               gelu_pre: torch.Tensor | None = None, gelu_deriv: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x . W^T for W = cat(ws, 0) (+ residual).  GELU epilogue when ``gelu_pre`` (receives the
+    pre-activation) or ``gelu_deriv`` (receives gelu'(pre-activation), for the backward) is given."""
     M, K = x2.shape
     seg = ws[0].shape[0]
     N = seg * len(ws)
@@ -139,22 +140,27 @@ def linear_fwd(x2: torch.Tensor, ws: list, *, residual: torch.Tensor | None = No
         if w.shape != (seg, K) or not w.is_contiguous():
             raise ValueError(f"weight of shape {tuple(w.shape)} does not match input width {K}")
     y = _rows(M, N, x2)
+    aux_out = gelu_pre if gelu_pre is not None else gelu_deriv
+    epi = H.RH_EPI_GELU if gelu_pre is not None else (H.RH_EPI_GELU_DERIV if gelu_deriv is not None else H.RH_EPI_NONE)
     gemm(H.RH_GEMM_NT, M, N, K, x2, _ld(x2), ws, K, [y], _ld(y),
          beta=0.0 if residual is None else 1.0, C=residual, ldc=0 if residual is None else _ld(residual),
-         epilogue=H.RH_EPI_GELU if gelu_pre is not None else H.RH_EPI_NONE,
-         aux_out=gelu_pre, ldaux=0 if gelu_pre is None else _ld(gelu_pre), b_seg_rows=seg if len(ws) > 1 else 0)
+         epilogue=epi, aux_out=aux_out, ldaux=0 if aux_out is None else _ld(aux_out),
+         b_seg_rows=seg if len(ws) > 1 else 0)
     return y
 
 
-def linear_dgrad(dy2: torch.Tensor, ws: list, *, gelu_pre: torch.Tensor | None = None) -> torch.Tensor:
-    """dx = dy . W for W = cat(ws, 0); times gelu'(gelu_pre) when given."""
+def linear_dgrad(dy2: torch.Tensor, ws: list, *, gelu_pre: torch.Tensor | None = None,
+                 gelu_deriv: torch.Tensor | None = None) -> torch.Tensor:
+    """dx = dy . W for W = cat(ws, 0); times gelu'(gelu_pre), or times the stored derivative
+    ``gelu_deriv``, when given."""
     M, N_out = dy2.shape
     seg = ws[0].shape[0]
     K_in = ws[0].shape[1]
     dx = _rows(M, K_in, dy2)
+    aux = gelu_pre if gelu_pre is not None else gelu_deriv
+    epi = H.RH_EPI_GELU_GRAD if gelu_pre is not None else (H.RH_EPI_MUL_AUX if gelu_deriv is not None else H.RH_EPI_NONE)
     gemm(H.RH_GEMM_NN, M, K_in, N_out, dy2, _ld(dy2), ws, K_in, [dx], _ld(dx),
-         epilogue=H.RH_EPI_GELU_GRAD if gelu_pre is not None else H.RH_EPI_NONE,
-         aux=gelu_pre, ldaux=0 if gelu_pre is None else _ld(gelu_pre), b_seg_rows=seg if len(ws) > 1 else 0)
+         epilogue=epi, aux=aux, ldaux=0 if aux is None else _ld(aux), b_seg_rows=seg if len(ws) > 1 else 0)
     return dx
 
 
@@ -444,20 +450,20 @@ class _MLPFn(torch.autograd.Function):
     def forward(ctx, x, w1, w2):
         H.require_gpu(x, w1, w2)
         x2 = _as_rows(x).contiguous()
-        u = _rows(x2.shape[0], w1.shape[0], x2)
-        h = linear_fwd(x2, [w1], gelu_pre=u)
+        gd = _rows(x2.shape[0], w1.shape[0], x2)  # gelu'(fc1 output), kept for the backward
+        h = linear_fwd(x2, [w1], gelu_deriv=gd)
         y = linear_fwd(h, [w2])
-        ctx.save_for_backward(x2, u, h)
+        ctx.save_for_backward(x2, gd, h)
         ctx.params = (w1, w2)
         ctx.shape = x.shape
         return y.view(*x.shape[:-1], w2.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
-        x2, u, h = ctx.saved_tensors
+        x2, gd, h = ctx.saved_tensors
         w1, w2 = ctx.params
         dy2 = _as_rows(dy).contiguous()
-        du = linear_dgrad(dy2, [w2], gelu_pre=u)
+        du = linear_dgrad(dy2, [w2], gelu_deriv=gd)
         linear_wgrad(dy2, h, [w2])
         dx = linear_dgrad(du, [w1]) if ctx.needs_input_grad[0] else None
         linear_wgrad(du, x2, [w1])
@@ -469,9 +475,10 @@ class _BlockFn(torch.autograd.Function):
     TP rank's shard of it with row-parallel partial sums (resihp/parallel/tp.py:260-265).
 
     Forward: LN1 -> fused QKV GEMM -> flash attention -> out GEMM with the residual add in its
-    epilogue -> LN2 -> fc1 GEMM with GELU epilogue -> fc2 GEMM with the residual add.
-    Backward reverses it; the residual-branch gradient is added inside the LayerNorm backward
-    kernels and GELU' inside the fc2 dgrad epilogue.
+    epilogue -> LN2 -> fc1 GEMM with GELU epilogue (which also stores gelu' of its input for the
+    backward) -> fc2 GEMM with the residual add.  Backward reverses it; the residual-branch
+    gradient is added inside the LayerNorm backward kernels and the stored gelu' is applied in
+    the fc2 dgrad epilogue.
     """
 
     @staticmethod
@@ -483,22 +490,22 @@ class _BlockFn(torch.autograd.Function):
         qkv, c, lse, head_dim = _attention_forward(n1, wq, wk, wv, num_heads, batch, seq)
         x1 = linear_fwd(c, [wo], residual=x2)
         n2, mu2, rs2 = ln_fwd(x1, g2, b2, eps)
-        u = _rows(x2.shape[0], w1.shape[0], x2)
-        h = linear_fwd(n2, [w1], gelu_pre=u)
+        gd = _rows(x2.shape[0], w1.shape[0], x2)  # gelu'(fc1 output), kept for the backward
+        h = linear_fwd(n2, [w1], gelu_deriv=gd)
         out = linear_fwd(h, [w2], residual=x1)
-        ctx.save_for_backward(x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, u, h)
+        ctx.save_for_backward(x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, gd, h)
         ctx.params = (g1, b1, wq, wk, wv, wo, g2, b2, w1, w2)
         ctx.meta = (batch, seq, num_heads, head_dim)
         return out.view(batch, seq, dim)
 
     @staticmethod
     def backward(ctx, dout):
-        x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, u, h = ctx.saved_tensors
+        x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, gd, h = ctx.saved_tensors
         g1, b1, wq, wk, wv, wo, g2, b2, w1, w2 = ctx.params
         batch, seq, num_heads, head_dim = ctx.meta
         d2 = _as_rows(dout).contiguous()
         # MLP branch
-        du = linear_dgrad(d2, [w2], gelu_pre=u)
+        du = linear_dgrad(d2, [w2], gelu_deriv=gd)
         linear_wgrad(d2, h, [w2])
         dn2 = linear_dgrad(du, [w1])
         linear_wgrad(du, n2, [w1])

@@ -106,6 +106,40 @@ def test_gemm_epilogues(cuda, gemm_tile, dtype):
     x = R.float().requires_grad_(True)
     F.gelu(x).backward(acc)
     assert rel_inf(D, x.grad) <= tol
+    # GELU_DERIV: aux_out = gelu'(pre-activation), D = gelu(pre)
+    G = torch.empty(M, N, dtype=dtype, device=cuda)
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D], N, epilogue=H.RH_EPI_GELU_DERIV, aux_out=G, ldaux=N)
+    pre = acc.clone().requires_grad_(True)
+    F.gelu(pre).backward(torch.ones_like(acc))
+    assert rel_inf(D, F.gelu(acc)) <= tol
+    assert rel_inf(G, pre.grad) <= tol
+    # MUL_AUX: D = acc * aux
+    ops.gemm(H.RH_GEMM_NT, M, N, K, A, K, [B], K, [D], N, epilogue=H.RH_EPI_MUL_AUX, aux=R, ldaux=N)
+    assert rel_inf(D, acc * R.float()) <= tol
+
+
+@pytest.mark.parametrize("K", [64, 96])
+def test_gemm_bf16_rounding_matches_torch(cuda, K):
+    """The bf16 store rounds to nearest even exactly like torch's float->bfloat16 conversion:
+    D[m, n] = hi[n] + lo[n] is an exact fp32 sum (two bf16 terms of a one-hot-pair product)
+    whose bf16 rounding is compared bit for bit, ties and negative values included.
+    K = 64 takes the direct-to-LDS kernel, K = 96 the register-staged one."""
+    g = torch.Generator().manual_seed(40)
+    N = 256
+    hi = torch.cat([torch.ones(64), -torch.ones(32), torch.randn(160, generator=g) * 100]).to(torch.bfloat16)
+    # low parts around the bf16 rounding boundary of hi: exact ties (2^-8 * |hi|), just above/below
+    rel = torch.tensor([0.5, 0.75, 0.25, 0.5 + 2 ** -6, 0.5 - 2 ** -6, 1.5, -0.5, -0.75])
+    lo = (hi.float().abs() * 2 ** -7 * rel.repeat(N // len(rel))).to(torch.bfloat16)
+    A = torch.zeros(64, K, dtype=torch.bfloat16)
+    A[:, 0] = 1.0
+    A[:, 1] = 1.0
+    B = torch.zeros(N, K, dtype=torch.bfloat16)
+    B[:, 0] = hi
+    B[:, 1] = lo
+    want = (hi.float() + lo.float()).to(torch.bfloat16).expand(64, N)
+    D = torch.empty(64, N, dtype=torch.bfloat16, device=cuda)
+    ops.gemm(H.RH_GEMM_NT, 64, N, K, A.to(cuda), K, [B.to(cuda)], K, [D], N)
+    assert torch.equal(D.cpu().view(torch.int16), want.contiguous().view(torch.int16))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
