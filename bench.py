@@ -278,6 +278,22 @@ WORKLOADS = {
 # ---------------------------------------------------------------------------
 # measurement
 # ---------------------------------------------------------------------------
+def _measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary of this
+    workload (profiles/<workload>_counters.md, line `traffic_bytes_per_launch <kernel> = N`):
+    FETCH_SIZE + WRITE_SIZE of a --pmc run, each scaled by what the same counter reads for a
+    copy of known size.  None when the summary does not cover this kernel."""
+    path = ROOT / "profiles" / f"{workload}_counters.md"
+    if not path.exists():
+        return None
+    key = f"traffic_bytes_per_launch {kernel} ="
+    for line in path.read_text().splitlines():
+        line = line.strip().strip("`")
+        if line.startswith(key):
+            return float(line[len(key):].strip())
+    return None
+
+
 def _physical_cores() -> int:
     try:
         n = len(os.sched_getaffinity(0))
@@ -295,6 +311,9 @@ def main(argv=None):
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB with the library's copy kernel (copy_kernel<16>): a transfer of "
+                         "known size that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build computes one rank's shard per GPU with no collectives "
@@ -306,6 +325,16 @@ def main(argv=None):
     from resihp import profiling
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration > 0:
+        from resihp.parallel.reshard import device_cat
+
+        src = torch.empty(args.copy_calibration * (1 << 20) // 2, dtype=torch.bfloat16, device=dev).view(-1, 4096)
+        src.fill_(1.0)
+        for _ in range(3):
+            device_cat([src], 0)
+        torch.cuda.synchronize()
+        _log(f"[bench] copy calibration: 3 copies of {args.copy_calibration} MiB (copy_kernel<16>)")
+        del src
     wl = WORKLOADS[args.workload]()
     _log(f"[bench] workload {wl.name}: setup")
     wl.setup(dev)
@@ -367,11 +396,14 @@ def main(argv=None):
     torch.cuda.synchronize()
     kernels = profiling.summary(events)
     n_steps = min(args.steps, 5)
-    dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    # dominant = the MFMA kernel with the most time per step (the split-K reduce is a separate,
+    # bandwidth-bound kernel with no FLOPs of its own)
+    dominant = max((k for k in kernels if kernels[k]["flops"] > 0), key=lambda k: kernels[k]["total_ms"])
     dk = kernels[dominant]
     achieved = dk["tflops"]
     roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12,
-                "unit": "TFLOP/s", "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved * 1e12 / PEAK_BF16, 4),
+                "traffic": _measured_traffic(wl.name, dominant),
                 "launches_per_step": dk["launches"] // n_steps, "mean_launch_us": round(dk["mean_ms"] * 1e3, 2),
                 "flops_per_launch": dk["flops_per_launch"]}
     per_kernel = {k: {"launches_per_step": v["launches"] // n_steps, "mean_us": round(v["mean_ms"] * 1e3, 2),

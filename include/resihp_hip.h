@@ -115,6 +115,20 @@ typedef struct rh_gemm_desc {
 int rh_gemm_workspace_bytes(const rh_gemm_desc* desc, int64_t* bytes);
 /* A smaller workspace than requested is legal: the call then runs unsplit. */
 int rh_gemm(const rh_gemm_desc* desc, void* workspace, int64_t workspace_bytes, void* stream);
+/* rh_gemm in two enqueued halves: RH_GEMM_STAGE_MAIN runs the main kernel (for a split-K
+ * plan it writes the fp32 partials to the workspace), RH_GEMM_STAGE_REDUCE then sums the
+ * partials and applies the epilogue (a no-op for an unsplit plan); RH_GEMM_STAGE_ALL is
+ * rh_gemm.  Both halves must see the same descriptor, workspace and stream order.  No
+ * counterpart in the reference: it lets profilers time the two kernels apart and callers
+ * schedule other work between them. */
+#define RH_GEMM_STAGE_ALL 0
+#define RH_GEMM_STAGE_MAIN 1
+#define RH_GEMM_STAGE_REDUCE 2
+int rh_gemm_stage(const rh_gemm_desc* desc, void* workspace, int64_t workspace_bytes, int stage, void* stream);
+/* Name of the main-kernel instantiation rh_gemm launches for this descriptor with the queried
+ * workspace (as rocprof prints it, e.g. "gemm_bf16_dma<256, 256, 2, 4, 0, 0, false>"), for
+ * attributing profiler records.  No counterpart in the reference (profiling support). */
+int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t len);
 
 /* ---- causal self-attention core ---------------------------------------------
  * Replaces  scores = q @ k^T / sqrt(Dh); masked_fill(triu(ones,1), -inf);

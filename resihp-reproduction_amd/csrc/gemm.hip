@@ -36,6 +36,7 @@
 // wgrad shapes), grid.z partitions K, each split writes fp32 partials to the
 // caller's workspace, and a reduce kernel sums them in split order
 // (deterministic) and applies the epilogue.
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <type_traits>
@@ -923,7 +924,14 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   p.aligned = al ? 1 : 0;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
-  p.group_m = 8;
+  // Each XCD receives a contiguous run of ~tiles/8 logical tiles (tile_coords); grouping that
+  // many tiles into a square-ish block of GROUP_M rows x (run/GROUP_M) columns minimises the A and
+  // B panels one XCD's L2 has to fetch (measured: 8 x 1 blocks of the 2048x2048 wgrad tiles
+  // fetched 1.5x the panels of 2 x 4 blocks).
+  const int64_t per_xcd = rh_cdiv((int64_t)pl.tiles_m * pl.tiles_n, 8);
+  int gm = 1;
+  while ((int64_t)(2 * gm) * (2 * gm) <= per_xcd && 2 * gm <= pl.tiles_m) gm *= 2;
+  p.group_m = gm;
   return p;
 }
 
@@ -967,7 +975,7 @@ void launch_main(int cfg, const GemmParams<T>& p, bool dma, dim3 grid, hipStream
 }
 
 template <typename T, int L, int EPI>
-int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st) {
+int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st, int stage) {
   GemmParams<T> p = make_params<T>(d, pl, ws);
   const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
   if (tiles > INT32_MAX) return rh_set_error(RH_ERR_INVALID, "rh_gemm: too many tiles (%lld)", (long long)tiles);
@@ -975,9 +983,11 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
   bool dma = false;
   if constexpr (std::is_same<T, bf16_t>::value) dma = dma_ok(d, pl, p);
   if (pl.splits > 1) {
-    launch_main<T, L, EPI, true>(pl.cfg, p, dma, grid, st);
-    int rc = rh_check_launch("rh_gemm");
-    if (rc) return rc;
+    if (stage != RH_GEMM_STAGE_REDUCE) {
+      launch_main<T, L, EPI, true>(pl.cfg, p, dma, grid, st);
+      int rc = rh_check_launch("rh_gemm");
+      if (rc || stage == RH_GEMM_STAGE_MAIN) return rc;
+    }
     const int64_t total = d->M * d->N;
     if constexpr (std::is_same<T, bf16_t>::value) {
       // every output row and the partials are 16-byte aligned when N % 8 == 0 (the partials
@@ -1001,27 +1011,28 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
     hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
     return rh_check_launch("rh_gemm split-k reduce");
   }
+  if (stage == RH_GEMM_STAGE_REDUCE) return RH_OK;  // unsplit: the main kernel did everything
   launch_main<T, L, EPI, false>(pl.cfg, p, dma, grid, st);
   return rh_check_launch("rh_gemm");
 }
 
 template <typename T, int EPI>
-int launch_epi(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st) {
+int launch_epi(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st, int stage) {
   switch (d->layout) {
-    case RH_GEMM_NT: return launch_layout<T, RH_GEMM_NT, EPI>(d, pl, ws, st);
-    case RH_GEMM_NN: return launch_layout<T, RH_GEMM_NN, EPI>(d, pl, ws, st);
-    default: return launch_layout<T, RH_GEMM_TN, EPI>(d, pl, ws, st);
+    case RH_GEMM_NT: return launch_layout<T, RH_GEMM_NT, EPI>(d, pl, ws, st, stage);
+    case RH_GEMM_NN: return launch_layout<T, RH_GEMM_NN, EPI>(d, pl, ws, st, stage);
+    default: return launch_layout<T, RH_GEMM_TN, EPI>(d, pl, ws, st, stage);
   }
 }
 
 template <typename T>
-int launch_dtype(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st) {
+int launch_dtype(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st, int stage) {
   switch (d->epilogue) {
-    case RH_EPI_NONE: return launch_epi<T, RH_EPI_NONE>(d, pl, ws, st);
-    case RH_EPI_GELU: return launch_epi<T, RH_EPI_GELU>(d, pl, ws, st);
-    case RH_EPI_GELU_GRAD: return launch_epi<T, RH_EPI_GELU_GRAD>(d, pl, ws, st);
-    case RH_EPI_GELU_DERIV: return launch_epi<T, RH_EPI_GELU_DERIV>(d, pl, ws, st);
-    default: return launch_epi<T, RH_EPI_MUL_AUX>(d, pl, ws, st);
+    case RH_EPI_NONE: return launch_epi<T, RH_EPI_NONE>(d, pl, ws, st, stage);
+    case RH_EPI_GELU: return launch_epi<T, RH_EPI_GELU>(d, pl, ws, st, stage);
+    case RH_EPI_GELU_GRAD: return launch_epi<T, RH_EPI_GELU_GRAD>(d, pl, ws, st, stage);
+    case RH_EPI_GELU_DERIV: return launch_epi<T, RH_EPI_GELU_DERIV>(d, pl, ws, st, stage);
+    default: return launch_epi<T, RH_EPI_MUL_AUX>(d, pl, ws, st, stage);
   }
 }
 
@@ -1039,6 +1050,33 @@ int launch_k0(const rh_gemm_desc* d, hipStream_t st) {
 
 }  // namespace
 
+extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t len) {
+  int rc = validate(desc);
+  if (rc) return rc;
+  RH_REQUIRE(buf != nullptr && len > 0, "rh_gemm_kernel_name: null or empty buffer");
+  if (desc->M == 0 || desc->N == 0) {
+    snprintf(buf, (size_t)len, "none");
+    return RH_OK;
+  }
+  if (desc->K == 0) {
+    snprintf(buf, (size_t)len, "gemm_splitk_reduce<%s, %d>", desc->dtype == RH_DTYPE_BF16 ? "unsigned short" : "float",
+             desc->epilogue);
+    return RH_OK;
+  }
+  const Plan pl = plan_gemm(desc);
+  const char* split = pl.splits > 1 ? "true" : "false";
+  if (desc->dtype != RH_DTYPE_BF16) {
+    snprintf(buf, (size_t)len, "gemm_f32_fma<%d, %d, %s>", desc->layout, desc->epilogue, split);
+    return RH_OK;
+  }
+  const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
+  static const int waves[3][2] = {{2, 4}, {4, 2}, {2, 2}};
+  snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma_ok(desc, pl, p) ? "gemm_bf16_dma" : "gemm_bf16_mfma",
+           kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, waves[pl.cfg][0], waves[pl.cfg][1], desc->layout, desc->epilogue,
+           split);
+  return RH_OK;
+}
+
 extern "C" int rh_gemm_workspace_bytes(const rh_gemm_desc* desc, int64_t* bytes) {
   int rc = validate(desc);
   if (rc) return rc;
@@ -1048,12 +1086,19 @@ extern "C" int rh_gemm_workspace_bytes(const rh_gemm_desc* desc, int64_t* bytes)
 }
 
 extern "C" int rh_gemm(const rh_gemm_desc* desc, void* workspace, int64_t workspace_bytes, void* stream) {
+  return rh_gemm_stage(desc, workspace, workspace_bytes, RH_GEMM_STAGE_ALL, stream);
+}
+
+extern "C" int rh_gemm_stage(const rh_gemm_desc* desc, void* workspace, int64_t workspace_bytes, int stage,
+                             void* stream) {
   int rc = validate(desc);
   if (rc) return rc;
+  RH_REQUIRE(stage >= RH_GEMM_STAGE_ALL && stage <= RH_GEMM_STAGE_REDUCE, "rh_gemm_stage: unknown stage %d", stage);
   if (desc->M == 0 || desc->N == 0) return RH_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf16 = desc->dtype == RH_DTYPE_BF16;
   if (desc->K == 0) {
+    if (stage == RH_GEMM_STAGE_REDUCE) return RH_OK;
     switch (desc->epilogue) {
       case RH_EPI_NONE: return bf16 ? launch_k0<bf16_t, RH_EPI_NONE>(desc, st) : launch_k0<float, RH_EPI_NONE>(desc, st);
       case RH_EPI_GELU: return bf16 ? launch_k0<bf16_t, RH_EPI_GELU>(desc, st) : launch_k0<float, RH_EPI_GELU>(desc, st);
@@ -1070,5 +1115,6 @@ extern "C" int rh_gemm(const rh_gemm_desc* desc, void* workspace, int64_t worksp
     pl.k_per_split = rh_cdiv(desc->K, bf16 ? kBK : fBK) * (bf16 ? kBK : fBK);
     pl.ws_bytes = 0;
   }
-  return bf16 ? launch_dtype<bf16_t>(desc, pl, workspace, st) : launch_dtype<float>(desc, pl, workspace, st);
+  return bf16 ? launch_dtype<bf16_t>(desc, pl, workspace, st, stage)
+              : launch_dtype<float>(desc, pl, workspace, st, stage);
 }

@@ -34,6 +34,9 @@ RH_EPI_GELU_GRAD = 2
 RH_EPI_GELU_DERIV = 3
 RH_EPI_MUL_AUX = 4
 
+RH_GEMM_STAGE_MAIN = 1
+RH_GEMM_STAGE_REDUCE = 2
+
 RH_MAX_SEG = 4
 
 c_i64 = ctypes.c_int64
@@ -87,6 +90,8 @@ _SIGNATURES = {
     "rh_version": [],
     "rh_gemm_workspace_bytes": [ctypes.POINTER(rh_gemm_desc), ctypes.POINTER(c_i64)],
     "rh_gemm": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_ptr],
+    "rh_gemm_stage": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_int, c_ptr],
+    "rh_gemm_kernel_name": [ctypes.POINTER(rh_gemm_desc), ctypes.c_char_p, c_i64],
     "rh_attn_fwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_float,
                     c_int, c_ptr],
     "rh_attn_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],

@@ -121,10 +121,15 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
     nbytes = H.query("rh_gemm_workspace_bytes", ctypes.byref(desc))
     ws = H.workspace(nbytes, dev)
     if profiling.active():
-        kind = "gemm_bf16_mfma" if desc.dtype == H.RH_DTYPE_BF16 else "gemm_f32_fma"
-        label = f"{kind}<{layout}, {epilogue}, {'true' if nbytes else 'false'}>"
-        with profiling.launch(label, 2.0 * M * N * K):
-            H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
+        # main kernel and split-K reduce timed apart (the reduce is a bandwidth kernel)
+        name = ctypes.create_string_buffer(128)
+        H.call("rh_gemm_kernel_name", ctypes.byref(desc), name, 128)
+        with profiling.launch(name.value.decode(), 2.0 * M * N * K):
+            H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_MAIN, H.stream_of(A))
+        if nbytes:
+            with profiling.launch("gemm_splitk_reduce", 0.0):
+                H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_REDUCE,
+                       H.stream_of(A))
         return
     H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
 
@@ -249,7 +254,7 @@ def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int)
     lse = torch.empty((batch, heads, seq), dtype=torch.float32, device=qkv.device)
     es = qkv.element_size()
     base = qkv.data_ptr()
-    with profiling.launch(f"attn_fwd<{head_dim}>", attn_flops(batch, seq, heads, head_dim)):
+    with profiling.launch(f"attn_fwd_mfma<{head_dim}>", attn_flops(batch, seq, heads, head_dim)):
         _attn_fwd_call(qkv, batch, seq, heads, head_dim, dl, es, base, ctx, lse)
     return ctx, lse
 
@@ -274,7 +279,8 @@ def attn_bwd(dctx: torch.Tensor, qkv: torch.Tensor, ctx: torch.Tensor, lse: torc
     base, dbase = qkv.data_ptr(), dqkv.data_ptr()
     nbytes = H.query("rh_attn_bwd_workspace_bytes", batch, seq, heads)
     ws = H.workspace(nbytes, qkv.device)
-    with profiling.launch(f"attn_bwd<{head_dim}>", 2.0 * attn_flops(batch, seq, heads, head_dim)):
+    with profiling.launch(f"attn_bwd_dq_mfma<{head_dim}> + attn_bwd_dkdv_mfma<{head_dim}>",
+                          2.0 * attn_flops(batch, seq, heads, head_dim)):
         H.call("rh_attn_bwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es,
                base + 2 * dl * es, _ld(qkv), ctx.data_ptr(), dl, dctx.data_ptr(), _ld(dctx), lse.data_ptr(), dbase,
                dbase + dl * es, dbase + 2 * dl * es, 3 * dl, 1.0 / math.sqrt(head_dim), 1, H.ptr(ws), nbytes,

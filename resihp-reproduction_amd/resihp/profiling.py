@@ -64,3 +64,73 @@ def summary(events) -> dict:
         d["flops_per_launch"] = d["flops"] / d["launches"]
         d["tflops"] = d["flops"] / (d["total_ms"] * 1e-3) / 1e12 if d["total_ms"] > 0 else 0.0
     return out
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 database summaries (python -m resihp.profiling ...)
+# ---------------------------------------------------------------------------
+def _short_name(name: str) -> str:
+    """'void (anonymous namespace)::gemm_bf16_dma<...>((anonymous namespace)::GemmParams<...>)'
+    -> 'gemm_bf16_dma<...>'."""
+    n = name.replace("void (anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return n[:i]
+    return n
+
+
+def kernel_table(db_path: str, steps: int) -> str:
+    """Markdown table of a --kernel-trace --stats database: calls, mean and per-step time."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    rows = con.execute("select name, total_calls, total_duration, average from top_kernels").fetchall()
+    out = ["| kernel | calls | mean us | us per step | % |", "|---|---:|---:|---:|---:|"]
+    total = sum(r[2] for r in rows)
+    for name, calls, dur, avg in rows:
+        out.append(f"| `{_short_name(name)}` | {calls} | {avg:.1f} | {dur / steps:.1f} | {100 * dur / total:.1f} |")
+    out.append(f"| **all kernels** | | | **{total / steps:.1f}** | |")
+    return "\n".join(out)
+
+
+def counter_table(db_path: str) -> dict:
+    """{kernel: {counter: mean per dispatch}} of a --pmc database (counters summed over the
+    hardware instances of each dispatch)."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    q = ("select dispatch_id, kernel_name, counter_name, sum(value) from counters_collection "
+         "group by dispatch_id, counter_name")
+    acc: dict = {}
+    for _, kname, cname, value in con.execute(q):
+        d = acc.setdefault(_short_name(kname), {}).setdefault(cname, [])
+        d.append(value)
+    return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in acc.items()}
+
+
+def _main(argv=None) -> int:
+    import argparse
+    import json
+
+    ap = argparse.ArgumentParser(prog="python -m resihp.profiling")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    k = sub.add_parser("kernels", help="markdown kernel table of a --kernel-trace --stats run")
+    k.add_argument("db")
+    k.add_argument("--steps", type=int, default=1, help="steps the trace covers (for per-step times)")
+    c = sub.add_parser("counters", help="per-kernel mean counter values of a --pmc run (JSON)")
+    c.add_argument("db")
+    args = ap.parse_args(argv)
+    if args.cmd == "kernels":
+        print(kernel_table(args.db, args.steps))
+    else:
+        print(json.dumps(counter_table(args.db), indent=1, sort_keys=True))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(_main())

@@ -118,6 +118,36 @@ def test_gemm_epilogues(cuda, gemm_tile, dtype):
     assert rel_inf(D, acc * R.float()) <= tol
 
 
+def test_gemm_stages_equal_one_call(cuda):
+    """rh_gemm_stage MAIN then REDUCE (a split-K plan) gives exactly rh_gemm's result."""
+    import ctypes
+
+    M, N, K = 512, 768, 8192  # TN wgrad shape with few tiles: the planner splits K
+    A = _rand(K, M, seed=50)
+    B = _rand(K, N, seed=51)
+    outs = []
+    for staged in (False, True):
+        D = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+        desc = H.rh_gemm_desc()
+        desc.dtype, desc.layout, desc.epilogue = H.RH_DTYPE_BF16, H.RH_GEMM_TN, H.RH_EPI_NONE
+        desc.b_nseg = desc.d_nseg = 1
+        desc.M, desc.N, desc.K = M, N, K
+        desc.A, desc.lda, desc.B[0], desc.ldb, desc.D[0], desc.ldd = A.data_ptr(), M, B.data_ptr(), N, D.data_ptr(), N
+        desc.alpha = 1.0
+        nbytes = H.query("rh_gemm_workspace_bytes", ctypes.byref(desc))
+        assert nbytes > 0
+        ws = H.workspace(nbytes, cuda)
+        if staged:
+            H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_MAIN, None)
+            H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_REDUCE, None)
+        else:
+            H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, None)
+        torch.cuda.synchronize()
+        outs.append(D)
+    assert torch.equal(outs[0], outs[1])
+    assert rel_inf(outs[0], A.float().t() @ B.float()) <= BF16_TOL
+
+
 @pytest.mark.parametrize("K", [64, 96])
 def test_gemm_bf16_rounding_matches_torch(cuda, K):
     """The bf16 store rounds to nearest even exactly like torch's float->bfloat16 conversion:

@@ -54,6 +54,28 @@ def test_library_version_and_argument_errors():
         _hip.call("rh_layernorm_fwd", 0, 4, 0, None, None, None, 1e-5, None, None, None, None)
 
 
+def test_gemm_kernel_name_reports_the_planned_instantiation():
+    """Planning needs no GPU (an absent device counts as 256 CUs): the wgrad of the 1.3B shard's
+    fc layers is a split-K direct-to-LDS TN GEMM, a ragged fp32 GEMM the FMA kernel."""
+    def name(dtype, layout, M, N, K, align=16):
+        d = _hip.rh_gemm_desc()
+        d.dtype, d.layout, d.M, d.N, d.K = dtype, layout, M, N, K
+        d.b_nseg = d.d_nseg = 1
+        d.A, d.B[0], d.D[0] = 0x10000, 0x20000 + align % 16, 0x30000
+        d.lda = M if layout == _hip.RH_GEMM_TN else K
+        d.ldb = K if layout == _hip.RH_GEMM_NT else N
+        d.ldd = N
+        d.alpha = 1.0
+        buf = ctypes.create_string_buffer(128)
+        _hip.call("rh_gemm_kernel_name", ctypes.byref(d), buf, 128)
+        return buf.value.decode()
+
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_TN, 2048, 2048, 8192) == "gemm_bf16_dma<256, 256, 2, 4, 2, 0, true>"
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048) == "gemm_bf16_dma<256, 256, 2, 4, 0, 0, false>"
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048, align=2).startswith("gemm_bf16_mfma<")
+    assert name(_hip.RH_DTYPE_F32, _hip.RH_GEMM_NN, 100, 77, 50) == "gemm_f32_fma<1, 0, false>"
+
+
 def test_gemm_descriptor_layout_matches_the_header():
     # int32 x6, then int64 M/N/K at offset 24; pointer arrays of RH_MAX_SEG
     assert _hip.rh_gemm_desc.M.offset == 24
