@@ -25,6 +25,10 @@
 //     block, lane i addresses row k0 + i/4, columns c0 + 4*(i%4) .. +3, and lane
 //     j receives rows k0..k0+3 of column c0 + j -- a k-major fragment without
 //     any scalar transposition.
+// Two epilogues (epilogue_sel picks one per call): LDS-staged (epilogue_tile_impl: the fp32 tile
+// goes through LDS so stores are 16-byte, whole-row runs) and from registers (epilogue_regs: a
+// DPP quad transpose gives each lane 4 consecutive columns of one output row; no LDS round trip,
+// no barrier, each wave finishes as soon as its own MFMAs retire).
 // Workgroup ids are remapped so that each XCD (ids are dealt round-robin over
 // the 8 XCDs) works on one contiguous run of a GROUP_M-grouped tile order:
 // tiles sharing A rows / B columns land in the same XCD's L2.
@@ -72,6 +76,8 @@ struct GemmParams {
   float* ws;            // split-K partials [splits][M][N]
   int64_t k_per_split;  // multiple of the k-tile
   int aligned;          // all rows 16-byte aligned -> vector loads
+  int out_vec;          // D/C/aux rows 8-byte aligned, split partials 16-byte aligned
+  int epi_lds;          // finish through LDS (epilogue_tile_impl) instead of epilogue_regs
   int tiles_m, tiles_n, group_m;
 };
 
@@ -318,6 +324,127 @@ __device__ __forceinline__ void mma_ktile(const bf16_t* a_s, const bf16_t* b_s, 
   }
 }
 
+// 4x4 transpose across the four lanes of each quad (DPP quad_perm, two exchange stages): on
+// entry lane s = lane % 4 holds v[t] = element (t, s) of a 4x4 block, on exit element (s, t).
+template <int CTRL>
+__device__ __forceinline__ float quad_perm_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
+  const bool b0 = lane & 1, b1 = lane & 2;
+#pragma unroll
+  for (int k = 0; k < 4; k += 2) {  // exchange bit 0 of (register, lane) with the neighbour lane ^ 1
+    const float got = quad_perm_f32<0xB1>(b0 ? v[k] : v[k + 1]);  // quad_perm [1,0,3,2]
+    if (b0) v[k] = got; else v[k + 1] = got;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {  // exchange bit 1 with lane ^ 2
+    const float got = quad_perm_f32<0x4E>(b1 ? v[k] : v[k + 2]);  // quad_perm [2,3,0,1]
+    if (b1) v[k] = got; else v[k + 2] = got;
+  }
+}
+
+// Register epilogue, no LDS and no barrier: each wave finishes its own WTM x WTN sub-tile as soon
+// as its last MFMA retires.  32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32)
+// + r%4, column l%32; a quad transpose turns every 4 registers into 4 consecutive columns of one
+// row, so C / aux reads and D / aux / partial writes are 8-byte (fp32 partials: 16-byte) vectors,
+// 64 contiguous bytes per row per instruction.  All C and aux reads are issued before any is
+// used.  Sub-tiles that cross the matrix edge (or unaligned rows) take the per-element path.
+template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int FM, int FN>
+__device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, floatx16_t (&acc)[FM][FN], int64_t m0,
+                                              int64_t n0, int wm, int wn, int lane) {
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  const int64_t wr0 = m0 + (int64_t)wm * WTM, wc0 = n0 + (int64_t)wn * WTN;
+  const int g = lane >> 5;
+  if (!(p.out_vec && wr0 + WTM <= p.M && wc0 + WTN <= p.N)) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = wr0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), n = wc0 + j * 32 + (lane & 31);
+          if (m >= p.M || n >= p.N) continue;
+          if (SPLIT)
+            p.ws[(int64_t)blockIdx.z * p.M * p.N + m * p.N + n] = acc[i][j][r];
+          else
+            epilogue_store<bf16_t, EPI>(p, m, n, acc[i][j][r]);
+        }
+    return;
+  }
+  // after the transpose: row wr0 + i*32 + 8*q + 4*g + lane%4, columns wc0 + j*32 + (lane & 28) + 0..3
+  const int64_t rl = wr0 + 4 * g + (lane & 3);
+  const int64_t cl = wc0 + (lane & 28);
+  if (SPLIT) {
+    float* ws = p.ws + (int64_t)blockIdx.z * p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          quad_transpose(v, lane);
+          const floatx4_t o = {v[0], v[1], v[2], v[3]};
+          *reinterpret_cast<floatx4_t*>(ws + (rl + i * 32 + 8 * q) * p.N + cl + j * 32) = o;
+        }
+    return;
+  }
+  constexpr bool kReadAux = epi_reads_aux<EPI>(), kWriteAux = epi_writes_aux<EPI>();
+  const bool has_c = p.beta != 0.f;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    // this row block's C and aux reads go out together, before any of them is used
+    u16x4_t cv[4][FN], av[4][FN];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = rl + i * 32 + 8 * q;
+      if (has_c) {
+        const bf16_t* crow = p.C ? p.C + m * p.ldc : d_row(p, m);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) cv[q][j] = *reinterpret_cast<const u16x4_t*>(crow + cl + j * 32);
+      }
+      if (kReadAux) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) av[q][j] = *reinterpret_cast<const u16x4_t*>(p.aux + m * p.ldaux + cl + j * 32);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = rl + i * 32 + 8 * q;
+      bf16_t* drow = d_row(p, m);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        quad_transpose(v, lane);
+        const int64_t n = cl + j * 32;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = has_c ? p.alpha * v[t] + p.beta * bf16_to_f32(cv[q][j][t]) : p.alpha * v[t];
+        if (kWriteAux) {
+          u16x4_t x;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const GeluParts gp = gelu_parts_fast(v[t]);
+            x[t] = f32_to_bf16(EPI == RH_EPI_GELU ? v[t] : gp.cdf + v[t] * gp.pdf);
+            v[t] *= gp.cdf;
+          }
+          *reinterpret_cast<u16x4_t*>(p.aux_out + m * p.ldaux + n) = x;
+        } else if (kReadAux) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float a = bf16_to_f32(av[q][j][t]);
+            v[t] *= EPI == RH_EPI_GELU_GRAD ? gelu_grad_fast_f(a) : a;
+          }
+        }
+        u16x4_t o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = f32_to_bf16(v[t]);
+        *reinterpret_cast<u16x4_t*>(drow + n) = o;
+      }
+    }
+  }
+}
+
 // Epilogue through LDS: the fp32 tile is written to LDS in row chunks, then every thread takes
 // 8 consecutive columns at a time -- one rolled loop, 16-byte coalesced loads and stores.
 // 32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
@@ -391,6 +518,22 @@ __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, 
     }
     __syncthreads();
   }
+}
+
+// Epilogue choice, measured per kernel inside the block's fwd+bwd step on MI355X: the LDS-staged
+// epilogue is faster for unsplit bf16 results without an aux read (its stores are whole 512-byte
+// row runs), the register epilogue for split-K partials and for the aux-reading forms.
+template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int SMEM_ELEMS, int FM, int FN>
+__device__ __forceinline__ void epilogue_sel(const GemmParams<bf16_t>& p, bf16_t* smem, floatx16_t (&acc)[FM][FN],
+                                             int64_t m0, int64_t n0, int wm, int wn, int lane) {
+  if constexpr (!SPLIT && !epi_reads_aux<EPI>()) {
+    if (p.epi_lds) {
+      __syncthreads();  // every wave is done reading the operand stages
+      epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, SMEM_ELEMS>(p, smem, acc, m0, n0, wm, wn, lane);
+      return;
+    }
+  }
+  epilogue_regs<BM, BN, WGM, WGN, EPI, SPLIT>(p, acc, m0, n0, wm, wn, lane);
 }
 
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
@@ -489,7 +632,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16
     }
   }
 
-  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
 }
 
 
@@ -666,7 +809,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
     __syncthreads();
   }
 
-  epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -922,12 +1065,25 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   // segment boundaries must not split a 16-byte chunk of the k-contiguous B or a k-tile row
   if (d->b_nseg > 1) al = al && d->b_seg_rows % 8 == 0;
   p.aligned = al ? 1 : 0;
+  // the register epilogue's vector path: 4-element bf16 groups of D / C / aux rows, 4-element
+  // fp32 groups of the [splits][M][N] partials
+  bool ov = d->ldd % 4 == 0 && (pl.splits == 1 || (d->N % 4 == 0 && rh_aligned(ws, 16)));
+  for (int s = 0; s < d->d_nseg; ++s) ov = ov && rh_aligned(d->D[s], 8);
+  if (d->beta != 0.f && d->C) ov = ov && rh_aligned(d->C, 8) && d->ldc % 4 == 0;
+  if (d->epilogue != RH_EPI_NONE) ov = ov && d->ldaux % 4 == 0;
+  if (d->aux) ov = ov && rh_aligned(d->aux, 8);
+  if (d->aux_out) ov = ov && rh_aligned(d->aux_out, 8);
+  if (d->d_nseg > 1) ov = ov && d->d_seg_rows % 4 == 0;
+  p.out_vec = ov ? 1 : 0;
+  // (epilogue_tile_impl checks the alignment of each 8-element chunk itself)
+  const bool lds = pl.splits == 1 && d->epilogue != RH_EPI_GELU_GRAD && d->epilogue != RH_EPI_MUL_AUX;
+  p.epi_lds = lds ? 1 : 0;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   // Each XCD receives a contiguous run of ~tiles/8 logical tiles (tile_coords); grouping that
   // many tiles into a square-ish block of GROUP_M rows x (run/GROUP_M) columns minimises the A and
-  // B panels one XCD's L2 has to fetch (measured: 8 x 1 blocks of the 2048x2048 wgrad tiles
-  // fetched 1.5x the panels of 2 x 4 blocks).
+  // B panels one XCD's L2 has to fetch (2 x 4 blocks of the 2048x2048 weight-gradient tiles need
+  // 6 panels where 8 x 1 blocks need 9).
   const int64_t per_xcd = rh_cdiv((int64_t)pl.tiles_m * pl.tiles_n, 8);
   int gm = 1;
   while ((int64_t)(2 * gm) * (2 * gm) <= per_xcd && 2 * gm <= pl.tiles_m) gm *= 2;
