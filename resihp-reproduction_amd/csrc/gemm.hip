@@ -639,33 +639,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16
 // ---------------------------------------------------------------------------
 // bf16 MFMA kernel fed by direct global->LDS loads
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Direct global->LDS load of 16 bytes per lane: lane l of the wave writes LDS bytes
-// lds_base + 16*l .. +15 (lds_base wave-uniform).  Issued through inline asm on purpose: the
-// compiler cannot see that the asynchronous LDS write never aliases the stages being read, and
-// with the builtin it waits for every outstanding load before each LDS read, serialising the
-// pipeline.  Completion is tracked explicitly with wait_vm_le (these loads count in vmcnt).
-__device__ __forceinline__ void dma16(const bf16_t* src, const bf16_t* lds_dst) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "s"(lds)
-      : "memory", "m0");
-}
-
-// wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
-// outstanding; they complete in issue order
-template <int N>
-__device__ __forceinline__ void wait_vm_le() {
-  static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
-}
-
 // The operand tiles go global->LDS with global_load_lds_dwordx4 (no staging registers, no LDS
 // write instructions).  k-tiles are 64 deep so that every k-contiguous row piece a load fetches
 // is a whole 128-byte cache line (measured on MI355X: the L2->CU path delivers ~1.5-2x more
