@@ -139,7 +139,8 @@ int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t len);
  * ptr + t*ld + h*head_dim + d.  lse is [batch, heads, seq] fp32, natural log of
  * the softmax denominator of each query row (saved by forward for backward).
  * `causal` = 1 masks keys after the query (the diagonal is kept), as the
- * reference always does; 0 attends to every key.
+ * reference always does; 0 attends to every key.  `scale` must be positive
+ * (the reference's 1/sqrt(head_dim)); other values are rejected (RH_ERR_INVALID).
  */
 int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
                 const void* q, const void* k, const void* v, int64_t ld_qkv,

@@ -497,7 +497,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
   __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
   static_assert((6 * DB * 16 * 64 + 1024) * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in an SGPR
   const int sub = w & 1, ph = w >> 1;
   const FragAddr<D> fa(lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
@@ -540,32 +540,38 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
         floatx16_t st = zero16();
 #pragma unroll
         for (int i = 0; i < KS; ++i) st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
-        const bool diag = a.causal && kt0 + 31 > wq0;
-        const bool tail = kt0 + 31 >= S;
-        float mx = -INFINITY;
+        // masks only where a key can lie past the query (diagonal stage) or past S (tail stage)
+        if ((a.causal && kt0 + 31 > wq0) || kt0 + 31 >= S) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
-          float sv = st[r] * c;
-          if ((tail && key >= S) || (diag && key > q_row)) sv = -INFINITY;
-          st[r] = sv;
-          mx = fmaxf(mx, sv);
+          for (int r = 0; r < 16; ++r) {
+            const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (key >= S || (a.causal && key > q_row)) st[r] = -INFINITY;
+          }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx);
-        const float corr = __builtin_amdgcn_exp2f(m - mnew);
-        lsum *= corr;
+        // row max on the raw scores (scale > 0), then in scaled log2 units
+        float mx = fmaxf(st[0], st[1]);
 #pragma unroll
-        for (int d = 0; d < DB; ++d)
+        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, st[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+        // Lazy rescaling: keep the running max while no row's max grows by more than 8 (so every
+        // p = 2^(s*c - m) stays <= 256, far inside fp32 and bf16 range); the final division by
+        // the row sum makes the result independent of which max was used.
+        if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+          const float mnew = fmaxf(m, mx);
+          const float corr = __builtin_amdgcn_exp2f(m - mnew);
+          lsum *= corr;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+          for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+          m = mnew;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(st[r] - mnew);
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[r], c, -m));
           st[r] = p;
           lsum += p;
         }
-        m = mnew;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t pb = pack8(st, s2);
@@ -621,7 +627,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
   __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
   static_assert(6 * DB * 16 * 64 * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in an SGPR
   const int sub = w & 1, ph = w >> 1;
   const FragAddr<D> fa(lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
@@ -683,13 +689,18 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
           st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
           dpt = mfma32(row_frag<D>(sV, 32 * ph, i, fa), doreg[i], dpt);
         }
-        const bool diag = a.causal && kt0 + 31 > wq0;
+        if ((a.causal && kt0 + 31 > wq0) || kt0 + 31 >= S || wq1 >= S) {  // diagonal or ragged stage
+          const bool diag = a.causal && kt0 + 31 > wq0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = qok && key < S && !(diag && key > q_row);
-          const float p = ok ? __builtin_amdgcn_exp2f(st[r] * c - lse2) : 0.f;
-          st[r] = p * (dpt[r] - del);
+          for (int r = 0; r < 16; ++r) {
+            const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            const bool ok = qok && key < S && !(diag && key > q_row);
+            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) : 0.f;
+            st[r] = p * (dpt[r] - del);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - del);
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
@@ -807,6 +818,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
           fd = nd;
         }
         const bool diag = a.causal && qt0 < wk0 + 31;
+        const bool ragged = diag || qt0 + 31 >= S || wk0 + 31 >= S;  // any element masked
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int qi0 = 32 * ph + 8 * r4 + 4 * g;
@@ -816,8 +828,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * r4 + j;
             const int q = q0 + qi0 + j;
-            const bool ok = q < S && key < S && !(diag && key > q);
-            const float p = ok ? __builtin_amdgcn_exp2f(sc[r] * c - lq[j]) : 0.f;
+            const bool ok = !ragged || (q < S && key < S && !(diag && key > q));
+            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lq[j])) : 0.f;
             dp[r] = p * (dp[r] - dq4[j]);
             sc[r] = p;
           }
@@ -927,6 +939,7 @@ extern "C" int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
   if (batch == 0 || seq == 0 || heads == 0) return RH_OK;
   RH_REQUIRE(q && k && v && o && lse, "rh_attn_fwd: null pointer");
   RH_REQUIRE(ld_qkv >= heads * head_dim && ld_o >= heads * head_dim, "rh_attn_fwd: leading dimension too small");
+  RH_REQUIRE(scale > 0.f, "rh_attn_fwd: scale must be positive (got %g)", (double)scale);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (mfma_ok(dtype, head_dim, {q, k, v, o}, {ld_qkv, ld_o})) {
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
@@ -967,6 +980,7 @@ extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
   if (rc) return rc;
   if (batch == 0 || seq == 0 || heads == 0) return RH_OK;
   RH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "rh_attn_bwd: null pointer");
+  RH_REQUIRE(scale > 0.f, "rh_attn_bwd: scale must be positive (got %g)", (double)scale);
   const int64_t width = heads * head_dim;
   RH_REQUIRE(ld_qkv >= width && ld_o >= width && ld_do >= width && ld_dqkv >= width,
              "rh_attn_bwd: leading dimension too small");
