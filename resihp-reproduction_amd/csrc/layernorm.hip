@@ -291,6 +291,125 @@ __global__ __launch_bounds__(256) void ln_bwd_bf16_kernel(int64_t rows, int dim,
   }
 }
 
+// bf16 rows of 1024 < dim <= 2048 (dim % 8 == 0): two waves share a row.  Wave p (= wave & 1)
+// of a pair owns the 16-byte chunks 64*C*p + lane + 64c (c < C), so each lane holds half the
+// row buffers and column partials of the one-wave kernel (registers for three to four waves per
+// SIMD instead of one).  The pair's partial row sums meet in LDS and are added part 0 + part 1
+// (fixed order); the LDS slot alternates with the iteration parity, so one barrier per row pair.
+template <int C>
+__global__ __launch_bounds__(256) void ln_bwd_bf16_pair_kernel(int64_t rows, int dim, const bf16_t* __restrict__ dy,
+                                                                const bf16_t* __restrict__ x,
+                                                                const float* __restrict__ mean,
+                                                                const float* __restrict__ rstd,
+                                                                const bf16_t* __restrict__ gamma,
+                                                                const bf16_t* __restrict__ dres,
+                                                                bf16_t* __restrict__ dx, float* __restrict__ part_g,
+                                                                float* __restrict__ part_b) {
+  __shared__ float rsum[2][4][2];               // [parity][wave][s1, s2]
+  __shared__ float red[2][2][2][64 * 8];        // [g/b][part][row slot][column of the chunk]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave & 1, slot = wave >> 1;
+  const int cbase = 64 * C * part;
+  const u16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+  bool ok[C];
+  u16x8_t gm[C];
+  float pg[C][8], pb[C][8];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    ok[c] = 8 * (cbase + lane + 64 * c) < dim;
+    gm[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(gamma + 8 * (cbase + lane + 64 * c)) : z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pg[c][j] = pb[c][j] = 0.f;
+  }
+  const int64_t stride = (int64_t)gridDim.x * 2;
+  auto load = [&](int64_t row, u16x8_t(&a)[C], u16x8_t(&b)[C], u16x8_t(&r)[C]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t off = row * dim + 8 * (cbase + lane + 64 * c);
+      a[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(dy + off) : z;
+      b[c] = ok[c] ? *reinterpret_cast<const u16x8_t*>(x + off) : z;
+      r[c] = (ok[c] && dres) ? *reinterpret_cast<const u16x8_t*>(dres + off) : z;
+    }
+  };
+  u16x8_t a[C], b[C], r[C];
+  {
+    const int64_t row = (int64_t)blockIdx.x * 2 + slot;
+    if (row < rows) load(row, a, b, r);
+  }
+  int parity = 0;
+  // every wave of the block runs the same iterations (the barrier); rows past the end idle
+  for (int64_t r0 = (int64_t)blockIdx.x * 2; r0 < rows; r0 += stride, parity ^= 1) {
+    const int64_t row = r0 + slot;
+    const bool valid = row < rows;
+    u16x8_t na[C], nb[C], nr[C];
+    if (row + stride < rows) load(row + stride, na, nb, nr);
+    const float mu = valid ? mean[row] : 0.f, rs = valid ? rstd[row] : 0.f;
+    float s1 = 0.f, s2 = 0.f;
+    if (valid) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float dv = bf16_to_f32(a[c][j]);
+          const float h = (bf16_to_f32(b[c][j]) - mu) * rs;
+          const float g = dv * bf16_to_f32(gm[c][j]);
+          s1 += g;
+          s2 += g * h;
+          pg[c][j] += dv * h;
+          pb[c][j] += dv;
+        }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    if (lane == 0) {
+      rsum[parity][wave][0] = s1;
+      rsum[parity][wave][1] = s2;
+    }
+    __syncthreads();
+    const float m1 = (rsum[parity][2 * slot][0] + rsum[parity][2 * slot + 1][0]) / (float)dim;
+    const float m2 = (rsum[parity][2 * slot][1] + rsum[parity][2 * slot + 1][1]) / (float)dim;
+    if (valid) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (!ok[c]) continue;
+        u16x8_t o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float h = (bf16_to_f32(b[c][j]) - mu) * rs;
+          const float g = bf16_to_f32(a[c][j]) * bf16_to_f32(gm[c][j]);
+          o[j] = f32_to_bf16(rs * (g - m1 - h * m2) + bf16_to_f32(r[c][j]));
+        }
+        *reinterpret_cast<u16x8_t*>(dx + row * dim + 8 * (cbase + lane + 64 * c)) = o;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      a[c] = na[c];
+      b[c] = nb[c];
+      r[c] = nr[c];
+    }
+  }
+  // column partials: the two row slots of each part are added slot 0 + slot 1
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      red[0][part][slot][lane * 8 + j] = pg[c][j];
+      red[1][part][slot][lane * 8 + j] = pb[c][j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * 64 * 8; i += 256) {
+      const int pt = i / (64 * 8), k = i % (64 * 8);
+      const int col = 8 * (64 * C * pt + k / 8 + 64 * c) + k % 8;
+      if (col < dim) {
+        part_g[(int64_t)blockIdx.x * dim + col] = red[0][pt][0][k] + red[0][pt][1][k];
+        part_b[(int64_t)blockIdx.x * dim + col] = red[1][pt][0][k] + red[1][pt][1][k];
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Column sums of the per-block partial rows: a block owns 64 columns; its 16 waves sum
 // partial rows w, w+16, ... for their lane's column, and the 16 wave sums are added in wave
 // order (fixed order: deterministic).  16 waves x 32 blocks keep enough loads in flight.
@@ -382,7 +501,10 @@ int launch_bwd_bf16(int64_t rows, int dim, const void* dy, const void* x, const 
                      (const bf16_t*)x, mean, rstd, (const bf16_t*)gamma, (const bf16_t*)dres, (bf16_t*)dx, pg, pb)
   if (chunks <= 1) RH_LN_BWD(1);
   else if (chunks <= 2) RH_LN_BWD(2);
-  else RH_LN_BWD(4);
+  else  // dim <= 2048: two waves per row
+    hipLaunchKernelGGL((ln_bwd_bf16_pair_kernel<2>), dim3((unsigned)nb), dim3(256), 0, st, rows, dim,
+                       (const bf16_t*)dy, (const bf16_t*)x, mean, rstd, (const bf16_t*)gamma, (const bf16_t*)dres,
+                       (bf16_t*)dx, pg, pb);
 #undef RH_LN_BWD
   return rh_check_launch("rh_layernorm_bwd");
 }

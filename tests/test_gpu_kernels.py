@@ -248,7 +248,11 @@ def test_attention_forward_backward(cuda, dtype, head_dim, seq, heads, batch):
 
 @pytest.mark.parametrize("dtype,rows,dim", [(torch.float32, 64, 64), (torch.float32, 37, 100),
                                             (torch.bfloat16, 512, 2048), (torch.bfloat16, 130, 768),
-                                            (torch.float32, 8, 5000), (torch.bfloat16, 3, 24)])
+                                            (torch.float32, 8, 5000), (torch.bfloat16, 3, 24),
+                                            # two waves per row (1024 < dim <= 2048): ragged dim,
+                                            # odd rows, a last row pair with one row
+                                            (torch.bfloat16, 37, 1544), (torch.bfloat16, 8193, 2048),
+                                            (torch.bfloat16, 1, 1032)])
 def test_layernorm_forward_backward(cuda, dtype, rows, dim):
     x = _rand(rows, dim, dtype=dtype, seed=30, scale=2.0) + 0.5
     w = torch.nn.Parameter(_rand(dim, dtype=dtype, seed=31) * 0.2 + 1.0)
