@@ -902,12 +902,12 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_vec(GemmParams<bf16_t>
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-enum TileCfg { kT256x256 = 0, kT256x128 = 1, kT128x128 = 2, kTf32 = 3 };
+enum TileCfg { kT256x256 = 0, kT256x128 = 1, kT128x128 = 2, kT256x192 = 3, kTf32 = 4 };
 
 struct TileShape {
   int bm, bn, threads;
 };
-constexpr TileShape kShapes[4] = {{256, 256, 512}, {256, 128, 512}, {128, 128, 256}, {fBM, fBN, 256}};
+constexpr TileShape kShapes[5] = {{256, 256, 512}, {256, 128, 512}, {128, 128, 256}, {256, 192, 512}, {fBM, fBN, 256}};
 
 struct Plan {
   int cfg;
@@ -918,8 +918,10 @@ struct Plan {
 };
 
 // Relative throughput of one CU on each tile shape (measured order of magnitude; bigger
-// tiles re-read less of A and B per FLOP).
-constexpr double kTileEff[3] = {1.0, 0.85, 0.6};
+// tiles re-read less of A and B per FLOP).  256x192 (NT only: both operands k-contiguous; the
+// m/n-contiguous LDS swizzle needs power-of-two widths) exists for N = 1536-type outputs, where
+// 256x256 tiles leave a quarter of the CUs idle.
+constexpr double kTileEff[4] = {1.0, 0.85, 0.6, 0.95};
 
 Plan plan_gemm(const rh_gemm_desc* d) {
   Plan pl{kTf32, 1, 0, 0, 0, 0};
@@ -930,17 +932,19 @@ Plan plan_gemm(const rh_gemm_desc* d) {
     return pl;
   }
   const int64_t cus = rh_device_cus();
-  // RESIHP_GEMM_TILE=0/1/2 pins the tile shape (256x256 / 256x128 / 128x128); tests use it to
-  // run every shape on every layout.
+  // RESIHP_GEMM_TILE=0/1/2/3 pins the tile shape (256x256 / 256x128 / 128x128 / 256x192, the
+  // last for NT only); tests use it to run every shape on every layout.
   int only = -1;
   if (const char* e = getenv("RESIHP_GEMM_TILE")) {
-    if (e[0] >= '0' && e[0] <= '2' && e[1] == 0) only = e[0] - '0';
+    if (e[0] >= '0' && e[0] <= '3' && e[1] == 0) only = e[0] - '0';
   }
+  if (only == kT256x192 && d->layout != RH_GEMM_NT) only = -1;
   // estimated time ~ (tiles resident per CU over the whole run) x tile area x k / efficiency;
   // split K when one wave of tiles leaves CUs idle
   double best = 1e300;
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 0; c < 4; ++c) {
     if (only >= 0 && c != only) continue;
+    if (c == kT256x192 && d->layout != RH_GEMM_NT) continue;
     const int64_t tm = rh_cdiv(d->M, kShapes[c].bm), tn = rh_cdiv(d->N, kShapes[c].bn);
     const int64_t tiles = tm * tn;
     const int64_t per_cu = c == kT128x128 ? 2 : 1;  // co-resident workgroups (LDS-bound)
@@ -1075,6 +1079,9 @@ void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipSt
   switch (cfg) {
     case kT256x256: launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st); break;
     case kT256x128: launch_bf16<256, 128, 4, 2, L, EPI, SPLIT>(p, dma, grid, st); break;
+    case kT256x192:
+      if constexpr (L == RH_GEMM_NT) launch_bf16<256, 192, 4, 2, L, EPI, SPLIT>(p, dma, grid, st);
+      break;
     default: launch_bf16<128, 128, 2, 2, L, EPI, SPLIT>(p, dma, grid, st); break;
   }
 }
@@ -1199,7 +1206,7 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
     return RH_OK;
   }
   const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
-  static const int waves[3][2] = {{2, 4}, {4, 2}, {2, 2}};
+  static const int waves[4][2] = {{2, 4}, {4, 2}, {2, 2}, {4, 2}};
   snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma_ok(desc, pl, p) ? "gemm_bf16_dma" : "gemm_bf16_mfma",
            kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, waves[pl.cfg][0], waves[pl.cfg][1], desc->layout, desc->epilogue,
            split);

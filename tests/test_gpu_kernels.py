@@ -41,9 +41,10 @@ def _gemm_ref(layout, A, B):
 SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8, 8), (513, 257, 1000)]
 
 
-@pytest.fixture(params=["auto", "0", "1", "2"])
+@pytest.fixture(params=["auto", "0", "1", "2", "3"])
 def gemm_tile(request, monkeypatch):
-    """Pin the bf16 GEMM tile shape (256x256 / 256x128 / 128x128) or let the planner choose."""
+    """Pin the bf16 GEMM tile shape (256x256 / 256x128 / 128x128 / 256x192, the last for NT
+    only) or let the planner choose."""
     if request.param == "auto":
         monkeypatch.delenv("RESIHP_GEMM_TILE", raising=False)
     else:

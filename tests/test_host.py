@@ -72,6 +72,9 @@ def test_gemm_kernel_name_reports_the_planned_instantiation():
 
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_TN, 2048, 2048, 8192) == "gemm_bf16_dma<256, 256, 2, 4, 2, 0, true>"
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048) == "gemm_bf16_dma<256, 256, 2, 4, 0, 0, false>"
+    # N = 1536 (the q|k|v projection): 256x192 tiles, exactly one per CU
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 1536, 2048) == "gemm_bf16_dma<256, 192, 4, 2, 0, 0, false>"
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NN, 8192, 1536, 2048).startswith("gemm_bf16_dma<256, ")
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048, align=2).startswith("gemm_bf16_mfma<")
     assert name(_hip.RH_DTYPE_F32, _hip.RH_GEMM_NN, 100, 77, 50) == "gemm_f32_fma<1, 0, false>"
 
