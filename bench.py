@@ -64,6 +64,10 @@ class Workload:
         for p in self.params():
             p.grad = None
 
+    def extra(self, dev) -> dict:
+        """Additional measured legs of this workload, merged into the JSON line."""
+        return {}
+
     def release(self):
         """Drop the last step's outputs, and with them its autograd graph."""
         self.out = None
@@ -266,12 +270,63 @@ class PPStage(ShardBlock):
         return [p.grad for p in self.params()]
 
 
+class ReshardShard(ShardBlock):
+    """The TP=2 rank-1 shard of a d2048 / FFN 8192 block after a TP4 -> TP2 reshard: the step is
+    the shard's fwd+bwd; the pack (repack_shards of one layer's four TP4 shards of every matrix
+    into both TP2 shards, on device) is measured as its own HBM-bound leg."""
+
+    def extra(self, dev):
+        import torch
+
+        from resihp.parallel.reshard import RepackPlan
+
+        d, ff = self.d, 4 * self.d
+        g = torch.Generator().manual_seed(3)
+        # (full shape, shard dim) of the per-layer matrices (reference reshard.py layer shard dims)
+        mats = {"q": ((d, d), 0), "k": ((d, d), 0), "v": ((d, d), 0), "fc1": ((ff, d), 0), "out": ((d, d), 1),
+                "fc2": ((d, ff), 1)}
+        shards = {n: [t.contiguous() for t in torch.chunk((torch.randn(*shape, generator=g) * 0.02).to(dev, torch.bfloat16),
+                                                          4, dim)] for n, (shape, dim) in mats.items()}
+
+        # destinations and the copy list prepared once; each pack is one batched copy launch
+        plan = RepackPlan([(shards[n], mats[n][1]) for n in mats], (0, 1), 2)
+
+        def pack():
+            outs = plan.run()
+            return [x for pair in zip(outs[0], outs[1]) for x in pair]
+
+        out = pack()
+        k = 0
+        for n in mats:
+            full = torch.cat(shards[n], mats[n][1])
+            for r in range(2):
+                if not torch.equal(out[k], torch.chunk(full, 2, mats[n][1])[r]):
+                    raise RuntimeError(f"reshard pack of {n} rank {r} differs from torch.cat/chunk")
+                k += 1
+        moved = 2 * sum(t.numel() * t.element_size() for t in out)  # each byte read once, written once
+        for _ in range(3):
+            pack()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        iters = 20
+        ev[0].record()
+        for _ in range(iters):
+            pack()
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) / iters * 1e3
+        gbps = moved / us / 1e3
+        return {"reshard_pack": {"bytes_moved": moved, "us": round(us, 2), "GB/s": round(gbps, 1),
+                                 "hbm_frac": round(gbps / 8000.0, 4), "bit_exact": True,
+                                 "what": "TP4->TP2 pack (RepackPlan, one launch) of one d2048/FFN8192 layer (q,k,v,fc1 dim 0; out,fc2 dim 1), both new ranks"}}
+
+
 WORKLOADS = {
     "tp4_shard_gpt1.3b_block": lambda: ShardBlock("tp4_shard_gpt1.3b_block"),
     "gpt2_small_lm": GPT2Small,
     "pp_stage_1f1b": PPStage,
-    "tp2_shard_after_reshard": lambda: ShardBlock("tp2_shard_after_reshard", d=2048, heads=16, tp=2, rank=1,
-                                                  seq=2048, batch=2),
+    "tp2_shard_after_reshard": lambda: ReshardShard("tp2_shard_after_reshard", d=2048, heads=16, tp=2, rank=1,
+                                                    seq=2048, batch=2),
 }
 
 
@@ -441,6 +496,7 @@ def main(argv=None):
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }
+    line.update(wl.extra(dev))
     print(json.dumps(line), flush=True)
     return 0
 

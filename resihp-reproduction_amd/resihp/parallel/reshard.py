@@ -219,3 +219,77 @@ def repack_shards(old_shards: list, shard_dim, new_rank: int, new_size: int) -> 
         piece = pieces[0]
         return device_clone(piece) if any(piece is o for o in old) else piece
     return device_cat(pieces, shard_dim)
+
+
+
+class RepackPlan:
+    """A prepared re-slice: for every (old_shards, shard_dim) item and every rank in `new_ranks`,
+    the destination tensor is allocated and the copy list built once; ``run()`` is then ONE
+    batched copy launch (rh_copy2d_batch) for every piece of every tensor -- a whole layer's
+    TP re-slice as a single HBM-bound kernel.  ``outs[r]`` are rank r's new shards, byte-identical
+    to ``repack_shards(shards, dim, r, new_size)`` (so to local_slice of the torch.cat)."""
+
+    def __init__(self, items: list, new_ranks, new_size: int):
+        self.outs = {}
+        segs = []
+        self._like = None
+        olds = []
+        for old_shards, shard_dim in items:
+            old = [t.detach().contiguous() for t in old_shards]
+            H.require_gpu(*old)
+            if shard_dim is not None:
+                for t in old:
+                    for d in range(t.dim()):
+                        if d != shard_dim and t.shape[d] != old[0].shape[d]:
+                            raise ValueError(f"shard shapes {tuple(old[0].shape)} and {tuple(t.shape)} differ "
+                                             f"off dim {shard_dim}")
+            olds.append((old, shard_dim))
+            self._like = old[0]
+        for r in new_ranks:
+            outs = []
+            for old, shard_dim in olds:
+                es = old[0].element_size()
+                if shard_dim is None:
+                    out = torch.empty_like(old[0])
+                    if out.numel():
+                        nb = out.numel() * es
+                        segs.append((old[0].data_ptr(), out.data_ptr(), nb, nb, 1, nb))
+                    outs.append(out)
+                    continue
+                total = sum(t.shape[shard_dim] for t in old)
+                start, stop = _chunk_bounds(total, new_size)[r]
+                shape = list(old[0].shape)
+                shape[shard_dim] = stop - start
+                out = torch.empty(shape, dtype=old[0].dtype, device=old[0].device)
+                outer, _, inner = _split_shape(shape, shard_dim)
+                off = 0
+                for t in old:
+                    e = t.shape[shard_dim]
+                    lo, hi = max(start, off), min(stop, off + e)
+                    if hi > lo and outer and inner:
+                        segs.append((t.data_ptr() + (lo - off) * inner * es,
+                                     out.data_ptr() + (lo - start) * inner * es,
+                                     e * inner * es, (stop - start) * inner * es, outer, (hi - lo) * inner * es))
+                    off += e
+                outs.append(out)
+            self.outs[r] = outs
+        self._olds = olds  # the sources stay alive as long as the plan
+        self._n = len(segs)
+        self._arr = (H.rh_copy2d * max(1, self._n))()
+        for i, (src, dst, src_ld, dst_ld, rows, row_bytes) in enumerate(segs):
+            self._arr[i].src, self._arr[i].dst = src, dst
+            self._arr[i].src_ld_bytes, self._arr[i].dst_ld_bytes = src_ld, dst_ld
+            self._arr[i].rows, self._arr[i].row_bytes = rows, row_bytes
+
+    def run(self) -> dict:
+        if self._n:
+            H.call("rh_copy2d_batch", self._arr, self._n, H.stream_of(self._like))
+        return self.outs
+
+
+def repack_many(items: list, new_rank: int, new_size: int) -> list:
+    """``[repack_shards(shards, dim, new_rank, new_size) for shards, dim in items]`` as one batched
+    copy launch (see RepackPlan)."""
+    if not items:
+        return []
+    return RepackPlan(items, (new_rank,), new_size).run()[new_rank]

@@ -364,6 +364,30 @@ def test_reshard_tp4_to_tp2_layer_at_full_size(cuda):
             assert torch.equal(got, torch.chunk(full, 2, dim)[new_rank]), name
 
 
+def test_reshard_repack_many_matches_per_tensor_repack(cuda):
+    """One batched launch for a whole layer (plus a 3-D tensor, a replicated one and ragged
+    old -> new degrees) equals repack_shards tensor by tensor, bit for bit."""
+    g = torch.Generator().manual_seed(62)
+    fulls = {"q": ((512, 256), 0), "out": ((256, 512), 1), "ln": ((256,), None), "t3": ((6, 10, 4), 1),
+             "odd": ((7, 9), 0)}
+    for old_n, new_n in ((4, 2), (3, 2), (2, 3)):
+        items, expect = [], []
+        for name, (shape, dim) in fulls.items():
+            full = (torch.randn(*shape, generator=g) * 10).to(torch.bfloat16).to(cuda)
+            if dim is None:
+                old = [full.clone()]
+            else:
+                if full.shape[dim] < old_n:
+                    continue
+                old = [t.contiguous() for t in torch.chunk(full, old_n, dim)]
+            items.append((old, dim))
+            expect.append([reshard.repack_shards(old, dim, r, new_n) for r in range(new_n)])
+        for r in range(new_n):
+            got = reshard.repack_many(items, r, new_n)
+            for i, t in enumerate(got):
+                assert torch.equal(t, expect[i][r]), (old_n, new_n, r, i)
+
+
 def test_reshard_unpack_entry_point(cuda):
     src = torch.arange(6 * 10, dtype=torch.int32, device=cuda).view(6, 10)
     outs = [torch.empty(6, e, dtype=torch.int32, device=cuda) for e in (3, 3, 4)]
