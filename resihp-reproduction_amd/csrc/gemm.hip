@@ -915,6 +915,8 @@ struct Plan {
   int64_t k_per_split;
   int64_t ws_bytes;
   int tiles_m, tiles_n;
+  int64_t k_main = 0;  // K covered by the `splits` slices (a k-tile multiple when tail == 1)
+  int tail = 0;        // 1: [k_main, K) is one more partial slice (register-staged kernel)
 };
 
 // Relative throughput of one CU on each tile shape (measured order of magnitude; bigger
@@ -929,6 +931,7 @@ Plan plan_gemm(const rh_gemm_desc* d) {
     pl.tiles_m = (int)rh_cdiv(d->M, fBM);
     pl.tiles_n = (int)rh_cdiv(d->N, fBN);
     pl.k_per_split = rh_cdiv(d->K, fBK) * fBK;
+    pl.k_main = d->K;
     return pl;
   }
   const int64_t cus = rh_device_cus();
@@ -939,6 +942,12 @@ Plan plan_gemm(const rh_gemm_desc* d) {
     if (e[0] >= '0' && e[0] <= '3' && e[1] == 0) only = e[0] - '0';
   }
   if (only == kT256x192 && d->layout != RH_GEMM_NT) only = -1;
+  // Ragged K (e.g. the LM head's backward, K = vocab): the bulk, a multiple of the k-tile, runs
+  // on the direct-to-LDS kernel and the last K % 64 as one extra fp32 partial slice on the
+  // register-staged kernel; the ordered reduce adds every slice, so the result is rounded once.
+  // (A k-row-segmented m/n-contiguous B keeps the one-kernel path.)
+  const bool tail = d->K % kBK != 0 && d->K >= 8 * kBK && (d->layout == RH_GEMM_NT || d->b_nseg == 1);
+  const int64_t Kp = tail ? d->K - d->K % kBK : d->K;
   // estimated time ~ (tiles resident per CU over the whole run) x tile area x k / efficiency;
   // split K when one wave of tiles leaves CUs idle
   double best = 1e300;
@@ -950,8 +959,8 @@ Plan plan_gemm(const rh_gemm_desc* d) {
     const int64_t per_cu = c == kT128x128 ? 2 : 1;  // co-resident workgroups (LDS-bound)
     const int64_t slots = cus * per_cu;
     for (int64_t splits = 1; splits <= 8; ++splits) {
-      if (splits > 1 && (d->K / splits < 512 || tiles * (splits - 1) >= slots)) break;
-      const int64_t kps = rh_cdiv(rh_cdiv(d->K, splits), kBK) * kBK;
+      if (splits > 1 && (Kp / splits < 512 || tiles * (splits - 1) >= slots)) break;
+      const int64_t kps = rh_cdiv(rh_cdiv(Kp, splits), kBK) * kBK;
       const int64_t waves = rh_cdiv(tiles * splits, slots);
       double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / kTileEff[c];
       // partial write + reduce: measured on MI355X, a split-4 2048x2048 reduce costs ~1/4 of a
@@ -960,14 +969,17 @@ Plan plan_gemm(const rh_gemm_desc* d) {
       if (t < best * 0.98) {
         best = t;
         pl.cfg = c;
-        pl.splits = (int)rh_cdiv(d->K, kps);
+        pl.splits = (int)rh_cdiv(Kp, kps);
         pl.k_per_split = kps;
         pl.tiles_m = (int)tm;
         pl.tiles_n = (int)tn;
       }
     }
   }
-  pl.ws_bytes = pl.splits > 1 ? (int64_t)pl.splits * d->M * d->N * (int64_t)sizeof(float) : 0;
+  pl.k_main = Kp;
+  pl.tail = tail ? 1 : 0;
+  const int64_t slices = pl.splits + pl.tail;
+  pl.ws_bytes = slices > 1 ? slices * d->M * d->N * (int64_t)sizeof(float) : 0;
   return pl;
 }
 
@@ -1044,7 +1056,7 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   p.aligned = al ? 1 : 0;
   // the register epilogue's vector path: 4-element bf16 groups of D / C / aux rows, 4-element
   // fp32 groups of the [splits][M][N] partials
-  bool ov = d->ldd % 4 == 0 && (pl.splits == 1 || (d->N % 4 == 0 && rh_aligned(ws, 16)));
+  bool ov = d->ldd % 4 == 0 && (pl.splits + pl.tail == 1 || (d->N % 4 == 0 && rh_aligned(ws, 16)));
   for (int s = 0; s < d->d_nseg; ++s) ov = ov && rh_aligned(d->D[s], 8);
   if (d->beta != 0.f && d->C) ov = ov && rh_aligned(d->C, 8) && d->ldc % 4 == 0;
   if (d->epilogue != RH_EPI_NONE) ov = ov && d->ldaux % 4 == 0;
@@ -1053,7 +1065,7 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   if (d->d_nseg > 1) ov = ov && d->d_seg_rows % 4 == 0;
   p.out_vec = ov ? 1 : 0;
   // (epilogue_tile_impl checks the alignment of each 8-element chunk itself)
-  const bool lds = pl.splits == 1 && d->epilogue != RH_EPI_GELU_GRAD && d->epilogue != RH_EPI_MUL_AUX;
+  const bool lds = pl.splits + pl.tail == 1 && d->epilogue != RH_EPI_GELU_GRAD && d->epilogue != RH_EPI_MUL_AUX;
   p.epi_lds = lds ? 1 : 0;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
@@ -1093,7 +1105,7 @@ bool dma_ok(const rh_gemm_desc* d, const Plan& pl, const GemmParams<bf16_t>& p) 
     const char* e = getenv("RESIHP_GEMM_DMA");
     return (e && e[0] == '0' && e[1] == 0) ? 0 : 1;
   }();
-  if (!enabled || !p.aligned || d->K % kBK || pl.k_per_split % kBK) return false;
+  if (!enabled || !p.aligned || pl.k_main % kBK || pl.k_per_split % kBK) return false;
   const bool a_kc = d->layout != RH_GEMM_TN, b_kc = d->layout == RH_GEMM_NT;
   if (!a_kc && (d->M < 8 || d->M % 8)) return false;
   if (!b_kc && (d->N < 8 || d->N % 8)) return false;
@@ -1116,13 +1128,29 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
   const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
   if (tiles > INT32_MAX) return rh_set_error(RH_ERR_INVALID, "rh_gemm: too many tiles (%lld)", (long long)tiles);
   dim3 grid((unsigned)tiles, 1, (unsigned)pl.splits);
+  const int slices = pl.splits + pl.tail;
+  p.K = pl.k_main;  // the split slices cover [0, k_main); a tail slice covers the rest
   bool dma = false;
   if constexpr (std::is_same<T, bf16_t>::value) dma = dma_ok(d, pl, p);
-  if (pl.splits > 1) {
+  if (slices > 1) {
     if (stage != RH_GEMM_STAGE_REDUCE) {
       launch_main<T, L, EPI, true>(pl.cfg, p, dma, grid, st);
       int rc = rh_check_launch("rh_gemm");
-      if (rc || stage == RH_GEMM_STAGE_MAIN) return rc;
+      if (rc) return rc;
+      if (pl.tail) {
+        // [k_main, K) into partial slice `splits`, operands offset by k_main along K
+        GemmParams<T> pt = p;
+        pt.K = d->K - pl.k_main;
+        pt.k_per_split = pt.K;
+        pt.A = L == RH_GEMM_TN ? p.A + pl.k_main * p.lda : p.A + pl.k_main;
+        for (int s = 0; s < RH_MAX_SEG; ++s)
+          pt.B[s] = L == RH_GEMM_NT ? p.B[s] + pl.k_main : p.B[s] + pl.k_main * p.ldb;
+        pt.ws = p.ws + (int64_t)pl.splits * d->M * d->N;
+        launch_main<T, L, EPI, true>(pl.cfg, pt, false, dim3((unsigned)tiles, 1, 1), st);
+        rc = rh_check_launch("rh_gemm (K tail)");
+        if (rc) return rc;
+      }
+      if (stage == RH_GEMM_STAGE_MAIN) return RH_OK;
     }
     const int64_t total = d->M * d->N;
     if constexpr (std::is_same<T, bf16_t>::value) {
@@ -1138,13 +1166,13 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
       if (vec) {
         int64_t blocks = rh_cdiv(total / 8, 256);
         if (blocks > 8 * 1024) blocks = 8 * 1024;
-        hipLaunchKernelGGL((gemm_splitk_reduce_vec<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
+        hipLaunchKernelGGL((gemm_splitk_reduce_vec<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
         return rh_check_launch("rh_gemm split-k reduce");
       }
     }
     int64_t blocks = rh_cdiv(total, 256);
     if (blocks > 4 * 1024) blocks = 4 * 1024;
-    hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, pl.splits);
+    hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
     return rh_check_launch("rh_gemm split-k reduce");
   }
   if (stage == RH_GEMM_STAGE_REDUCE) return RH_OK;  // unsplit: the main kernel did everything
@@ -1200,7 +1228,7 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
     return RH_OK;
   }
   const Plan pl = plan_gemm(desc);
-  const char* split = pl.splits > 1 ? "true" : "false";
+  const char* split = pl.splits + pl.tail > 1 ? "true" : "false";
   if (desc->dtype != RH_DTYPE_BF16) {
     snprintf(buf, (size_t)len, "gemm_f32_fma<%d, %d, %s>", desc->layout, desc->epilogue, split);
     return RH_OK;
@@ -1246,8 +1274,10 @@ extern "C" int rh_gemm_stage(const rh_gemm_desc* desc, void* workspace, int64_t 
     }
   }
   Plan pl = plan_gemm(desc);
-  if (pl.splits > 1 && (workspace == nullptr || workspace_bytes < pl.ws_bytes || !rh_aligned(workspace, 16))) {
+  if (pl.splits + pl.tail > 1 && (workspace == nullptr || workspace_bytes < pl.ws_bytes || !rh_aligned(workspace, 16))) {
     pl.splits = 1;
+    pl.tail = 0;
+    pl.k_main = desc->K;
     pl.k_per_split = rh_cdiv(desc->K, bf16 ? kBK : fBK) * (bf16 ? kBK : fBK);
     pl.ws_bytes = 0;
   }

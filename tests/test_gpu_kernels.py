@@ -38,7 +38,8 @@ def _gemm_ref(layout, A, B):
     return A32.t() @ B32
 
 
-SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8, 8), (513, 257, 1000)]
+SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8, 8), (513, 257, 1000),
+          (256, 384, 1000)]  # ragged K with aligned M/N: direct-to-LDS bulk + register-staged K tail
 
 
 @pytest.fixture(params=["auto", "0", "1", "2", "3"])

@@ -57,12 +57,12 @@ def test_library_version_and_argument_errors():
 def test_gemm_kernel_name_reports_the_planned_instantiation():
     """Planning needs no GPU (an absent device counts as 256 CUs): the wgrad of the 1.3B shard's
     fc layers is a split-K direct-to-LDS TN GEMM, a ragged fp32 GEMM the FMA kernel."""
-    def name(dtype, layout, M, N, K, align=16):
+    def name(dtype, layout, M, N, K, align=16, lda=None):
         d = _hip.rh_gemm_desc()
         d.dtype, d.layout, d.M, d.N, d.K = dtype, layout, M, N, K
         d.b_nseg = d.d_nseg = 1
         d.A, d.B[0], d.D[0] = 0x10000, 0x20000 + align % 16, 0x30000
-        d.lda = M if layout == _hip.RH_GEMM_TN else K
+        d.lda = lda or (M if layout == _hip.RH_GEMM_TN else K)
         d.ldb = K if layout == _hip.RH_GEMM_NT else N
         d.ldd = N
         d.alpha = 1.0
@@ -75,6 +75,9 @@ def test_gemm_kernel_name_reports_the_planned_instantiation():
     # N = 1536 (the q|k|v projection): 256x192 tiles, exactly one per CU
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 1536, 2048) == "gemm_bf16_dma<256, 192, 4, 2, 0, 0, false>"
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NN, 8192, 1536, 2048).startswith("gemm_bf16_dma<256, ")
+    # ragged K (LM head dgrad, K = vocab 50257, logits rows padded to 50264): the 64-aligned bulk
+    # on the direct-to-LDS kernel
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NN, 8192, 768, 50257, lda=50264).startswith("gemm_bf16_dma<")
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048, align=2).startswith("gemm_bf16_mfma<")
     assert name(_hip.RH_DTYPE_F32, _hip.RH_GEMM_NN, 100, 77, 50) == "gemm_f32_fma<1, 0, false>"
 
