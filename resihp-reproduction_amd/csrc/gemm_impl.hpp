@@ -396,6 +396,40 @@ __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, float
   }
   constexpr bool kReadAux = epi_reads_aux<EPI>(), kWriteAux = epi_writes_aux<EPI>();
   const bool has_c = p.beta != 0.f;
+  if constexpr (kReadAux) {
+    if (!has_c) {
+      // aux-reading epilogue without C (the fc2 dgrad times gelu'): the whole sub-tile's aux
+      // reads go out before the first is used (the main loop's registers are free by now)
+      u16x4_t av[FM][4][FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            av[i][q][j] = *reinterpret_cast<const u16x4_t*>(p.aux + (rl + i * 32 + 8 * q) * p.ldaux + cl + j * 32);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t m = rl + i * 32 + 8 * q;
+          bf16_t* drow = d_row(p, m);
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            quad_transpose(v, lane);
+            u16x4_t o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float a = bf16_to_f32(av[i][q][j][t]);
+              o[t] = f32_to_bf16(p.alpha * v[t] * (EPI == RH_EPI_GELU_GRAD ? gelu_grad_fast_f(a) : a));
+            }
+            *reinterpret_cast<u16x4_t*>(drow + cl + j * 32) = o;
+          }
+        }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     // this row block's C and aux reads go out together, before any of them is used

@@ -70,9 +70,12 @@ def summary(events) -> dict:
 # rocprofv3 database summaries (python -m resihp.profiling ...)
 # ---------------------------------------------------------------------------
 def _short_name(name: str) -> str:
-    """'void (anonymous namespace)::gemm_bf16_dma<...>((anonymous namespace)::GemmParams<...>)'
-    -> 'gemm_bf16_dma<...>'."""
-    n = name.replace("void (anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    """'void (anonymous namespace)::gemm_bf16_dma<...>((anonymous namespace)::GemmParams<...>)' or
+    'void rh_gemm_impl::gemm_bf16_dma<...>(rh_gemm_impl::GemmParams<...>)' -> 'gemm_bf16_dma<...>':
+    the return type, namespace qualifiers of the kernel and the parameter list are dropped."""
+    n = name.replace("(anonymous namespace)::", "")
+    if n.startswith("void "):
+        n = n[5:]
     depth = 0
     for i, ch in enumerate(n):
         if ch == "<":
@@ -80,7 +83,12 @@ def _short_name(name: str) -> str:
         elif ch == ">":
             depth -= 1
         elif ch == "(" and depth == 0:
-            return n[:i]
+            n = n[:i]
+            break
+    # namespace qualifiers before the template arguments: keep what follows the last '::' there
+    head = n.split("<", 1)[0]
+    if "::" in head:
+        n = n[len(head.rsplit("::", 1)[0]) + 2:]
     return n
 
 

@@ -192,3 +192,16 @@ def test_schedule_functions():
             pipeline_phases(bad[0], stage_index=bad[1], num_stages=bad[2])
     with pytest.raises(ValueError):
         pipeline_phases(-1, stage_index=0, num_stages=1)
+
+
+def test_profiling_short_name_strips_namespaces_and_parameters():
+    from resihp.profiling import _short_name
+
+    full = "void rh_gemm_impl::gemm_bf16_dma<256, 256, 2, 4, 2, 0, true>(rh_gemm_impl::GemmParams<unsigned short>)"
+    assert _short_name(full) == "gemm_bf16_dma<256, 256, 2, 4, 2, 0, true>"
+    anon = "void (anonymous namespace)::attn_fwd_mfma<128>((anonymous namespace)::AttnArgs<unsigned short>, int)"
+    assert _short_name(anon) == "attn_fwd_mfma<128>"
+    assert _short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+    # template arguments that name namespaced types are kept whole
+    torch_k = "void at::native::vectorized_elementwise_kernel<8, at::native::FillFunctor<float> >(int, float)"
+    assert _short_name(torch_k) == "vectorized_elementwise_kernel<8, at::native::FillFunctor<float> >"
