@@ -188,8 +188,19 @@ def linear_wgrad(dy2: torch.Tensor, x2: torch.Tensor, params: list) -> None:
             if not acc:
                 targets[i].zero_()
         accs = [True] * len(accs)
-    gemm(H.RH_GEMM_TN, N_out, K_in, M_rows, dy2, _ld(dy2), [x2], _ld(x2), targets, K_in,
-         beta=1.0 if accs[0] else 0.0, d_seg_rows=seg if len(params) > 1 else 0)
+    M_gemm, d_seg = N_out, (seg if len(params) > 1 else 0)
+    pad_rows = -N_out % 8
+    if (len(params) == 1 and pad_rows and dy2.dtype == torch.bfloat16 and _ld(dy2) >= N_out + pad_rows
+            and dy2.storage_offset() + (M_rows - 1) * _ld(dy2) + N_out + pad_rows
+            <= dy2.untyped_storage().nbytes() // dy2.element_size()):
+        # A ragged output count (the LM head's vocabulary, 50257) keeps the m-contiguous dy off the
+        # direct-to-LDS kernel.  dy's rows are padded in memory (the logits layout) and the padding
+        # lies inside its allocation, so the GEMM runs over the rounded count; the extra output rows
+        # land in a scratch segment and are dropped.
+        M_gemm, d_seg = N_out + pad_rows, N_out
+        targets = targets + [torch.empty(pad_rows, K_in, dtype=targets[0].dtype, device=targets[0].device)]
+    gemm(H.RH_GEMM_TN, M_gemm, K_in, M_rows, dy2, _ld(dy2), [x2], _ld(x2), targets, K_in,
+         beta=1.0 if accs[0] else 0.0, d_seg_rows=d_seg)
     for p, buf, w in zip(params, targets, want):
         if w:
             _finish_grad(p, buf)

@@ -204,6 +204,24 @@ def test_gemm_qkv_projection_at_shard_size(cuda):
     assert rel_inf(y, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("padded", [True, False])
+def test_linear_wgrad_ragged_outputs(cuda, padded):
+    """LM-head-style weight gradient: 50257 output rows.  With dy a view of rows padded to a
+    multiple of 8 (the logits layout) the GEMM runs over the rounded count into a scratch row
+    segment; without padding it takes the plain path.  Both equal the fp32 product, and a second
+    call accumulates."""
+    T, V, d = 128, 50257, 64
+    buf = _rand(T, V + 7, dtype=torch.bfloat16, seed=40, scale=0.01)
+    dy = buf[:, :V] if padded else buf[:, :V].contiguous()
+    x = _rand(T, d, dtype=torch.bfloat16, seed=41)
+    w = torch.nn.Parameter(torch.zeros(V, d, dtype=torch.bfloat16, device=cuda))
+    ops.linear_wgrad(dy, x, [w])
+    ref = dy.float().t() @ x.float()
+    assert rel_inf(w.grad, ref) <= BF16_TOL
+    ops.linear_wgrad(dy, x, [w])
+    assert rel_inf(w.grad, 2 * ref) <= BF16_TOL
+
+
 def _attn_ref(q, k, v, heads):
     """fp32 reference attention on [B, S, H*Dh] rows (the reference's explicit S x S form)."""
     B, S, W = q.shape
