@@ -46,45 +46,63 @@ __device__ __forceinline__ void store8(T* p, const float* v) {
 }
 
 // Row log-sum-exp.  VEC: row start 16-byte aligned -> 8-wide loads.
+// exp(x) as the hardware base-2 exponential of x*log2(e) (v_exp_f32, ~1 ulp): the online
+// log-sum-exp below runs in base-2 units (m2 = max * log2 e), one FMA + one v_exp per logit.
+constexpr float kLog2eX = 1.4426950408889634074f;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <typename T, bool VEC>
 __device__ float row_lse(const T* x, int64_t V, float* scratch) {
-  float m = -INFINITY, s = 0.f;
+  float m = -INFINITY, s = 0.f;  // m: running max in base-2 units; s: sum of 2^(x*log2e - m)
+  auto add = [&](float cm2, const float* v, int n) {
+    const float mn = fmaxf(m, cm2);
+    float acc = (m == -INFINITY) ? 0.f : s * exp2_hw(m - mn);
+    for (int t = 0; t < n; ++t) acc += exp2_hw(fmaf(v[t], kLog2eX, -mn));
+    s = acc;
+    m = mn;
+  };
   if (VEC) {
     const int64_t full = V / 8 * 8;
-    for (int64_t j = (int64_t)threadIdx.x * 8; j < full; j += kT * 8) {
+    int64_t j = (int64_t)threadIdx.x * 8;
+    // two 8-element chunks per trip: both loads in flight before the math
+    for (; j + kT * 8 < full; j += 2 * kT * 8) {
+      float v[8], w[8];
+      load8<T>(x + j, v);
+      load8<T>(x + j + kT * 8, w);
+      float cm = fmaxf(v[0], w[0]);
+#pragma unroll
+      for (int t = 1; t < 8; ++t) cm = fmaxf(cm, fmaxf(v[t], w[t]));
+      const float mn = fmaxf(m, cm * kLog2eX);
+      float acc = (m == -INFINITY) ? 0.f : s * exp2_hw(m - mn);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc += exp2_hw(fmaf(v[t], kLog2eX, -mn)) + exp2_hw(fmaf(w[t], kLog2eX, -mn));
+      s = acc;
+      m = mn;
+    }
+    for (; j < full; j += kT * 8) {
       float v[8];
       load8<T>(x + j, v);
       float cm = v[0];
 #pragma unroll
       for (int t = 1; t < 8; ++t) cm = fmaxf(cm, v[t]);
-      const float mn = fmaxf(m, cm);
-      float acc = s * expf(m - mn);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc += expf(v[t] - mn);
-      s = acc;
-      m = mn;
+      add(cm * kLog2eX, v, 8);
     }
-    for (int64_t j = full + threadIdx.x; j < V; j += kT) {
-      const float v = ld_f32(x + j);
-      const float mn = fmaxf(m, v);
-      s = s * expf(m - mn) + expf(v - mn);
-      m = mn;
+    for (int64_t k = full + threadIdx.x; k < V; k += kT) {
+      const float v = ld_f32(x + k);
+      add(v * kLog2eX, &v, 1);
     }
   } else {
-    for (int64_t j = threadIdx.x; j < V; j += kT) {
-      const float v = ld_f32(x + j);
-      const float mn = fmaxf(m, v);
-      s = s * expf(m - mn) + expf(v - mn);
-      m = mn;
+    for (int64_t k = threadIdx.x; k < V; k += kT) {
+      const float v = ld_f32(x + k);
+      add(v * kLog2eX, &v, 1);
     }
   }
   const float M = block_max(m, scratch);
-  const float part = (m == -INFINITY) ? 0.f : s * expf(m - M);
+  const float part = (m == -INFINITY) ? 0.f : s * exp2_hw(m - M);
   const float tot = block_sum(part, scratch + 8);
-  return M + logf(tot);
+  return (M + log2f(tot)) * 0.69314718055994530942f;  // natural-log units
 }
 
-// dlogits row: (exp(x - lse) - [j == tgt]) * scale over [0, V), zero on [V, ld_d).
 template <typename T, bool VEC>
 __device__ void row_grad(const T* x, T* d, int64_t V, int64_t ld_d, float lse, int64_t tgt, float scale) {
   if (VEC) {
