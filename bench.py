@@ -105,12 +105,34 @@ class ShardBlock(Workload):
                        "parallelism": f"one TP={tp} rank on 1 GPU, no collectives (row-parallel partial sums)"}
 
     def _state(self):
-        from oracle import torch_ref  # synthetic weights only (same generator as the tests)
+        """This rank's shard of seeded synthetic block weights: matrices N(0, 0.02) drawn from one
+        torch.Generator(seed 0) in parameter order, LayerNorm gamma = 1 / beta = 0, cut along the
+        reference's shard dims (q/k/v/fc1 rows, out/fc2 columns), bf16."""
         import torch
 
-        st = torch_ref.synthetic_state(self.d, self.layers, 8 * self.tp, self.seq, std=0.02, seed=0, first=False,
-                                       last=False, tp_size=self.tp, tp_rank=self.rank)
-        return {k: v.to(torch.bfloat16) for k, v in st.items()}
+        from resihp.parallel.reshard import shard_dims
+
+        g = torch.Generator().manual_seed(0)
+        d, f = self.d, 4 * self.d
+        full = {}
+        for gid in range(self.layers):
+            p = f"layers.{gid}."
+            full[p + "attn_norm.weight"] = torch.ones(d)
+            full[p + "attn_norm.bias"] = torch.zeros(d)
+            for n in ("q_proj", "k_proj", "v_proj", "out_proj"):
+                full[p + f"attn.{n}.weight"] = torch.randn(d, d, generator=g) * 0.02
+            full[p + "mlp_norm.weight"] = torch.ones(d)
+            full[p + "mlp_norm.bias"] = torch.zeros(d)
+            full[p + "mlp.fc1.weight"] = torch.randn(f, d, generator=g) * 0.02
+            full[p + "mlp.fc2.weight"] = torch.randn(d, f, generator=g) * 0.02
+        layout = shard_dims(range(self.layers))
+        out = {}
+        for k, v in full.items():
+            dim = layout[k]
+            if dim is not None and self.tp > 1:
+                v = torch.chunk(v, self.tp, dim)[self.rank].contiguous()
+            out[k] = v.to(torch.bfloat16)
+        return out
 
     def setup(self, dev):
         import torch
