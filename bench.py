@@ -167,7 +167,7 @@ class ShardBlock(Workload):
 
         st = {k: v.float().requires_grad_(True) for k, v in self._state().items()}
         g = torch.Generator().manual_seed(1)
-        mb = 1
+        mb = self.batch
         x = torch.randn(mb, self.seq, self.d, generator=g).requires_grad_(True)
         dy = torch.randn(mb, self.seq, self.d, generator=g) * 1e-2
 
@@ -177,17 +177,10 @@ class ShardBlock(Workload):
                                           is_last=False, hidden=x)
             out.backward(dy)
 
-        one()  # warm-up
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            one()
-            steps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or steps >= 20:
-                break
-        return {"tokens": mb * self.seq * steps, "seconds": el,
-                "sample": f"{steps} fwd+bwd of the same shard at micro-batch {mb} (seq {self.seq}), fp32, "
-                          f"oracle torch-CPU restatement"}
+        sec = _median_time(one, budget_s)
+        return {"tokens": mb * self.seq, "seconds": sec,
+                "sample": f"fwd+bwd of the same shard at micro-batch {mb} (seq {self.seq}, {self.layers} layer(s)), "
+                          f"fp32, oracle torch-CPU restatement; median of 3 after 1 warm-up"}
 
 
 class GPT2Small(Workload):
@@ -240,23 +233,17 @@ class GPT2Small(Workload):
 
         st = torch_ref.synthetic_state(self.d, self.layers, self.vocab, self.seq, std=0.02, seed=0)
         st = {k: v.requires_grad_(True) for k, v in st.items()}
-        bsz = 1
+        bsz = 2  # a quarter of the batch keeps the sample near 10 s
         tok = torch.randint(0, self.vocab, (bsz, self.seq), generator=torch.Generator().manual_seed(1))
 
         def one():
             logits = torch_ref.model_forward(st, tok, self.heads, range(self.layers))
             torch_ref.next_token_loss(logits, tok, self.vocab).backward()
 
-        one()
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            one()
-            steps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or steps >= 20:
-                break
-        return {"tokens": bsz * self.seq * steps, "seconds": el,
-                "sample": f"{steps} fwd+bwd of the whole LM at batch {bsz}, fp32, oracle torch-CPU restatement"}
+        sec = _median_time(one, budget_s)
+        return {"tokens": bsz * self.seq, "seconds": sec,
+                "sample": f"fwd+bwd of the whole LM at batch {bsz} of {self.batch} (seq {self.seq}), fp32, oracle "
+                          f"torch-CPU restatement; median of 3 after 1 warm-up"}
 
 
 class PPStage(ShardBlock):
@@ -291,6 +278,26 @@ class PPStage(ShardBlock):
     def outputs(self):
         return [p.grad for p in self.params()]
 
+    def cpu_sample(self, budget_s):
+        import torch
+
+        from oracle import torch_ref
+
+        st = {k: v.float().requires_grad_(True) for k, v in self._state().items()}
+        g = torch.Generator().manual_seed(2)
+        x = torch.randn(self.batch, self.seq, self.d, generator=g).requires_grad_(True)
+        dy = torch.randn(self.batch, self.seq, self.d, generator=g) * 1e-2
+
+        def one():
+            out = torch_ref.shard_forward(st, num_heads=self.heads, tp_rank=0, tp_size=1, vocab_size=8,
+                                          layer_ids=range(self.layers), is_first=False, is_last=False, hidden=x)
+            out.backward(dy)
+
+        sec = _median_time(one, budget_s)
+        return {"tokens": self.batch * self.seq, "seconds": sec,
+                "sample": f"one micro-batch ({self.batch}x{self.seq}) of the {self.layers}-layer stage, fwd+bwd, fp32, "
+                          f"oracle torch-CPU restatement; median of 3 after 1 warm-up"}
+
 
 class ReshardShard(ShardBlock):
     """The TP=2 rank-1 shard of a d2048 / FFN 8192 block after a TP4 -> TP2 reshard: the step is
@@ -298,49 +305,81 @@ class ReshardShard(ShardBlock):
     into both TP2 shards, on device) is measured as its own HBM-bound leg."""
 
     def extra(self, dev):
-        import torch
+        return {"reshard_pack": reshard_pack_leg(dev)}
 
-        from resihp.parallel.reshard import RepackPlan
 
-        d, ff = self.d, 4 * self.d
-        g = torch.Generator().manual_seed(3)
-        # (full shape, shard dim) of the per-layer matrices (reference reshard.py layer shard dims)
-        mats = {"q": ((d, d), 0), "k": ((d, d), 0), "v": ((d, d), 0), "fc1": ((ff, d), 0), "out": ((d, d), 1),
-                "fc2": ((d, ff), 1)}
-        shards = {n: [t.contiguous() for t in torch.chunk((torch.randn(*shape, generator=g) * 0.02).to(dev, torch.bfloat16),
-                                                          4, dim)] for n, (shape, dim) in mats.items()}
+def reshard_pack_leg(dev, reps=10):
+    """TP4 -> TP2 re-slice of one d2048 / FFN 8192 layer (q, k, v, fc1 split on dim 0; out, fc2 on
+    dim 1) into both new ranks' shards: one batched copy launch (RepackPlan), checked bit for bit
+    against torch.cat / torch.chunk, timed with a cold cache (a 1 GiB buffer, larger than L2 plus
+    the 256 MB Infinity Cache, is written before every pack)."""
+    import torch
 
-        # destinations and the copy list prepared once; each pack is one batched copy launch
-        plan = RepackPlan([(shards[n], mats[n][1]) for n in mats], (0, 1), 2)
+    from resihp.parallel.reshard import RepackPlan
 
-        def pack():
-            outs = plan.run()
-            return [x for pair in zip(outs[0], outs[1]) for x in pair]
+    d, ff = 2048, 8192
+    g = torch.Generator().manual_seed(3)
+    mats = {"q": ((d, d), 0), "k": ((d, d), 0), "v": ((d, d), 0), "fc1": ((ff, d), 0), "out": ((d, d), 1),
+            "fc2": ((d, ff), 1)}
+    shards = {n: [t.contiguous() for t in torch.chunk((torch.randn(*shape, generator=g) * 0.02).to(dev, torch.bfloat16),
+                                                      4, dim)] for n, (shape, dim) in mats.items()}
+    plan = RepackPlan([(shards[n], mats[n][1]) for n in mats], (0, 1), 2)
 
-        out = pack()
-        k = 0
-        for n in mats:
-            full = torch.cat(shards[n], mats[n][1])
-            for r in range(2):
-                if not torch.equal(out[k], torch.chunk(full, 2, mats[n][1])[r]):
-                    raise RuntimeError(f"reshard pack of {n} rank {r} differs from torch.cat/chunk")
-                k += 1
-        moved = 2 * sum(t.numel() * t.element_size() for t in out)  # each byte read once, written once
-        for _ in range(3):
-            pack()
-        torch.cuda.synchronize()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        iters = 20
+    def pack():
+        outs = plan.run()
+        return [x for pair in zip(outs[0], outs[1]) for x in pair]
+
+    out = pack()
+    k = 0
+    for n in mats:
+        full = torch.cat(shards[n], mats[n][1])
+        for r in range(2):
+            if not torch.equal(out[k], torch.chunk(full, 2, mats[n][1])[r]):
+                raise RuntimeError(f"reshard pack of {n} rank {r} differs from torch.cat/chunk")
+            k += 1
+    moved = 2 * sum(t.numel() * t.element_size() for t in out)  # each byte read once, written once
+    del out
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    evs = []
+    for _ in range(reps):
+        flush.fill_(1)
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         ev[0].record()
-        for _ in range(iters):
-            pack()
+        pack()
         ev[1].record()
-        torch.cuda.synchronize()
-        us = ev[0].elapsed_time(ev[1]) / iters * 1e3
-        gbps = moved / us / 1e3
-        return {"reshard_pack": {"bytes_moved": moved, "us": round(us, 2), "GB/s": round(gbps, 1),
-                                 "hbm_frac": round(gbps / 8000.0, 4), "bit_exact": True,
-                                 "what": "TP4->TP2 pack (RepackPlan, one launch) of one d2048/FFN8192 layer (q,k,v,fc1 dim 0; out,fc2 dim 1), both new ranks"}}
+        evs.append(ev)
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) for a, b in evs)[reps // 2] * 1e3
+    gbps = moved / us / 1e3
+    return {"bytes_per_launch": moved, "mean_us": round(us, 2), "GB/s": round(gbps, 1),
+            "hbm_frac": round(gbps * 1e9 / PEAK_HBM, 4), "bit_exact": True, "launches_per_step": 1,
+            "what": "TP4->TP2 pack (RepackPlan, one launch) of one d2048/FFN8192 layer, both new ranks; "
+                    "cold cache (1 GiB written before each pack), median of 10"}
+
+
+def xent_leg(dev, reps=5):
+    """Next-token cross-entropy with its gradient (rh_xent_fwd writing dlogits) at GPT-2-small's
+    rows: logits [8, 1024, 50257] bf16 (row stride 50264), targets uniform in [0, 50257)."""
+    import torch
+
+    from resihp import ops, profiling
+
+    batch, seq, vocab = 8, 1024, 50257
+    g = torch.Generator(device="cpu").manual_seed(5)
+    buf = torch.empty(batch * seq, 50264, dtype=torch.bfloat16, device=dev)
+    buf[:, :vocab] = (torch.randn(batch * seq, vocab, generator=g) * 2.0).to(dev, torch.bfloat16)
+    logits = buf[:, :vocab].view(batch, seq, vocab).requires_grad_(True)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g).to(dev)
+    ops.next_token_loss(logits, tokens, vocab)
+    torch.cuda.synchronize()
+    with profiling.record() as events:
+        for _ in range(reps):
+            ops.next_token_loss(logits, tokens, vocab)
+    torch.cuda.synchronize()
+    (label, k), = profiling.summary(events).items()
+    return {"bytes_per_launch": k["bytes_per_launch"], "mean_us": round(k["mean_ms"] * 1e3, 2),
+            "GB/s": round(k["gbps"], 1), "hbm_frac": round(k["gbps"] * 1e9 / PEAK_HBM, 4), "launches_per_step": 1,
+            "what": f"{label} at GPT-2-small rows (8x1024 tokens, vocab 50257, bf16), mean of {reps}"}
 
 
 WORKLOADS = {
@@ -359,24 +398,72 @@ def _measured_traffic(workload: str, kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary of this
     workload (profiles/<workload>_counters.md, line `traffic_bytes_per_launch <kernel> = N`):
     FETCH_SIZE + WRITE_SIZE of a --pmc run, each scaled by what the same counter reads for a
-    copy of known size.  None when the summary does not cover this kernel."""
+    copy of known size.  The summary records the sources digest of the library it measured
+    (`library_sources_sha256 = ...`); a summary of other sources, or one that does not cover this
+    kernel, gives (None, reason)."""
     path = ROOT / "profiles" / f"{workload}_counters.md"
     if not path.exists():
-        return None
+        return None, "no counter summary for this workload"
     key = f"traffic_bytes_per_launch {kernel} ="
+    stamp, value = None, None
     for line in path.read_text().splitlines():
         line = line.strip().strip("`")
+        if line.startswith("library_sources_sha256 ="):
+            stamp = line.split("=", 1)[1].strip()
         if line.startswith(key):
-            return float(line[len(key):].strip())
-    return None
+            value = float(line[len(key):].strip())
+    from resihp.profiling import library_sources_digest
+
+    if stamp != library_sources_digest():
+        return None, "counter summary measured other library sources"
+    if value is None:
+        return None, "counter summary does not cover this kernel"
+    return value, f"profiles/{path.name}"
 
 
-def _physical_cores() -> int:
+def _cpu_info() -> dict:
+    """Threads to use for the CPU baseline and what they are: the physical cores (distinct
+    package/core ids) of this process's affinity set, capped at the CPU share a GPU job gets here
+    (OMP_NUM_THREADS when set), and the CPU model name."""
     try:
-        n = len(os.sched_getaffinity(0))
+        cpus = sorted(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        cpus = list(range(os.cpu_count() or 1))
+    cores = set()
+    for c in cpus:
+        topo = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            cores.add((topo.joinpath("physical_package_id").read_text().strip(),
+                       topo.joinpath("core_id").read_text().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    physical = max(1, len(cores))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    use = min(physical, int(share)) if share.isdigit() and int(share) > 0 else physical
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"threads": use, "physical_cores_in_affinity": physical, "logical_cpus_in_affinity": len(cpus),
+            "model": model}
+
+
+def _median_time(fn, budget_s: float) -> float:
+    """1 warm-up call, then the median of 3 timed calls (fewer if one call exceeds the budget)."""
+    t0 = time.perf_counter()
+    fn()
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return sorted(times)[len(times) // 2]
 
 
 def main(argv=None):
@@ -388,6 +475,8 @@ def main(argv=None):
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-legs", action="store_true",
+                    help="skip the standalone cross-entropy and reshard-pack bandwidth legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB with the library's copy kernel (copy_kernel<16>): a transfer of "
                          "known size that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -478,23 +567,37 @@ def main(argv=None):
     dominant = max((k for k in kernels if kernels[k]["flops"] > 0), key=lambda k: kernels[k]["total_ms"])
     dk = kernels[dominant]
     achieved = dk["tflops"]
+    traffic, traffic_src = _measured_traffic(wl.name, dominant)
     roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12,
-                "unit": "TFLOP/s", "frac": round(achieved * 1e12 / PEAK_BF16, 4),
-                "traffic": _measured_traffic(wl.name, dominant),
+                "unit": "TFLOP/s", "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": traffic,
+                "traffic_source": traffic_src, "timing": "HIP events around each launch, 5 eager steps",
                 "launches_per_step": dk["launches"] // n_steps, "mean_launch_us": round(dk["mean_ms"] * 1e3, 2),
                 "flops_per_launch": dk["flops_per_launch"]}
     per_kernel = {k: {"launches_per_step": v["launches"] // n_steps, "mean_us": round(v["mean_ms"] * 1e3, 2),
-                      "tflops": round(v["tflops"], 1)} for k, v in sorted(kernels.items())}
+                      "tflops": round(v["tflops"], 1)} for k, v in sorted(kernels.items()) if v["flops"] > 0}
+    # bandwidth-bound kernels of the step: algorithmic bytes (inputs read once, outputs written
+    # once) over the HIP-event duration, against the 8 TB/s HBM peak
+    hbm = {k: {"launches_per_step": v["launches"] // n_steps, "mean_us": round(v["mean_ms"] * 1e3, 2),
+               "bytes_per_launch": int(v["bytes_per_launch"]), "GB/s": round(v["gbps"], 1),
+               "hbm_frac": round(v["gbps"] * 1e9 / PEAK_HBM, 4)}
+           for k, v in sorted(kernels.items()) if v["bytes"] > 0}
     _log("[bench] per-kernel: " + json.dumps(per_kernel))
+    _log("[bench] bandwidth kernels: " + json.dumps(hbm))
+    if args.workload == "tp4_shard_gpt1.3b_block" and not args.no_extra_legs:
+        # the path's other bandwidth kernels, measured in this run at their own workloads' sizes
+        hbm["xent_fwd (+ dlogits), GPT-2-small rows"] = xent_leg(dev)
+        hbm["reshard_pack, TP4->TP2 d2048/FFN8192 layer"] = reshard_pack_leg(dev)
+        _log("[bench] extra bandwidth legs done")
 
     cpu = None
     if not args.no_cpu_baseline:
-        cores = _physical_cores()
-        torch.set_num_threads(cores)
-        _log(f"[bench] CPU baseline on {cores} threads (budget {args.cpu_seconds}s)")
+        info = _cpu_info()
+        torch.set_num_threads(info["threads"])
+        _log(f"[bench] CPU baseline on {info['threads']} threads of {info['model']} (budget {args.cpu_seconds}s)")
         sample = wl.cpu_sample(args.cpu_seconds)
-        cpu = {"value": round(sample["tokens"] / sample["seconds"], 2), "unit": "tokens/s", "cores": cores,
-               "kind": "port", "sample": sample["sample"], "torch": torch.__version__}
+        cpu = {"value": round(sample["tokens"] / sample["seconds"], 2), "unit": "tokens/s", "cores": info["threads"],
+               "kind": "port", "sample": sample["sample"], "cpu_model": info["model"],
+               "physical_cores_in_affinity": info["physical_cores_in_affinity"], "torch": torch.__version__}
 
     line = {
         "metric": METRIC,
@@ -515,6 +618,7 @@ def main(argv=None):
         "algorithmic_flops_per_step": wl.flops,
         "roofline": roofline,
         "kernels": per_kernel,
+        "hbm": hbm,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }

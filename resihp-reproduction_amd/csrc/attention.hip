@@ -7,6 +7,13 @@
 //   dP_ij = do_i.v_j,  dS_ij = P_ij (dP_ij - delta_i)
 //   dq_i = scale sum_j dS_ij k_j,  dk_j = scale sum_i dS_ij q_i,  dv_j = sum_i P_ij do_i
 // P is rebuilt from lse in the backward; the [S,S] matrix never reaches HBM.
+// delta must equal sum_j P_ij dP_ij (the identity that makes every row of dS sum to zero,
+// so that dq_i = scale sum_j dS_ij (k_j - c) for any c): with bf16 outputs the forward also
+// stores the rounding residual o - bf16(o) (in bf16), and delta is formed from both parts.
+// From the rounded o alone, each row of dS sums to do_i.(o_i - bf16(o_i)) instead of zero
+// and dq / dk pick up that error times the keys' / queries' common component (measured:
+// ~2 % of the q/k projection gradients of a 12-layer GPT-2-small at its random init, 0.3 %
+// with the residual).
 //
 // bf16 / head_dim 64 or 128: MFMA kernels built on v_mfma_f32_32x32x16_bf16.
 // Scores are computed transposed (S^T = K Q^T, or S = Q K^T in the dK/dV kernel) so that
@@ -41,6 +48,8 @@ struct AttnArgs {
   int64_t ld_qkv;
   const T* o;
   T* o_out;
+  const T* o_lo;   // residual o - round(o) (bf16 only; may be null)
+  T* o_lo_out;
   int64_t ld_o;
   const T* dout;
   int64_t ld_do;
@@ -68,9 +77,10 @@ __global__ __launch_bounds__(256) void attn_delta(AttnArgs<T> a) {
   const int h = (int)(idx % a.H);
   const int64_t t = idx / a.H;
   const T* o = a.o + t * a.ld_o + (int64_t)h * a.D;
+  const T* olo = a.o_lo ? a.o_lo + t * a.ld_o + (int64_t)h * a.D : nullptr;
   const T* d = a.dout + t * a.ld_do + (int64_t)h * a.D;
   float s = 0.f;
-  for (int i = 0; i < a.D; ++i) s = fmaf(ld_f32(o + i), ld_f32(d + i), s);
+  for (int i = 0; i < a.D; ++i) s = fmaf(ld_f32(o + i) + (olo ? ld_f32(olo + i) : 0.f), ld_f32(d + i), s);
   const int64_t b = t / a.S, sq = t % a.S;
   a.delta_out[(b * a.H + h) * a.S + sq] = s;
 }
@@ -132,9 +142,14 @@ __global__ __launch_bounds__(gQ) void attn_fwd_generic(AttnArgs<T> a) {
   if (qi >= S) return;
   const float inv = 1.f / l;
   T* op = a.o_out + (tok0 + qi) * a.ld_o + (int64_t)h * D;
+  T* olo = a.o_lo_out ? a.o_lo_out + (tok0 + qi) * a.ld_o + (int64_t)h * D : nullptr;
 #pragma unroll
   for (int d = 0; d < DMAX; ++d)
-    if (d < D) st_f32(op + d, o[d] * inv);
+    if (d < D) {
+      const float v = o[d] * inv;
+      st_f32(op + d, v);
+      if (olo) st_f32(olo + d, v - ld_f32(op + d));
+    }
   a.lse_out[(int64_t)bh * S + qi] = (m + log2f(l)) * kLn2;
 }
 
@@ -443,6 +458,19 @@ __device__ __forceinline__ void st4(bf16_t* p, const floatx16_t& v, int rr, floa
   *reinterpret_cast<u16x4_t*>(p) = u;
 }
 
+// st4 plus the rounding residual of the same four values (bf16) at `lo`
+__device__ __forceinline__ void st4_split(bf16_t* p, bf16_t* lo, const floatx16_t& v, int rr, float mul) {
+  u16x4_t u, r;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float x = v[4 * rr + t] * mul;
+    u[t] = f32_to_bf16(x);
+    r[t] = f32_to_bf16(x - bf16_to_f32(u[t]));
+  }
+  *reinterpret_cast<u16x4_t*>(p) = u;
+  *reinterpret_cast<u16x4_t*>(lo) = r;
+}
+
 // Load the 8 k-slices (16 d each) of one head-row as MFMA operand registers: lane l holds
 // d = 16i + 8*(l/32) .. +7 of row `row` for slice i.
 template <int KS>
@@ -610,10 +638,19 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
       if (q_row < S) {
         const float inv = 1.f / lall;
         bf16_t* op = a.o_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
+        if (a.o_lo_out) {
+          bf16_t* olo = a.o_lo_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
 #pragma unroll
-        for (int d = 0; d < DB; ++d)
+          for (int d = 0; d < DB; ++d)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) st4(op + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
+            for (int rr = 0; rr < 4; ++rr)
+              st4_split(op + d * 32 + 8 * rr + 4 * g, olo + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
+        } else {
+#pragma unroll
+          for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) st4(op + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
+        }
         if (g == 0) a.lse_out[(int64_t)it.bh * S + q_row] = (mall + log2f(lall)) * kLn2;
       }
     }
@@ -649,13 +686,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     float del = 0.f;
     {
       const bf16_t* op = a.o + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
+      const bf16_t* olo = a.o_lo + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
+      const bool has_lo = a.o_lo != nullptr;
 #pragma unroll
       for (int i = 0; i < KS; ++i) {
         if (!qok) break;
         const u16x8_t ov = *reinterpret_cast<const u16x8_t*>(op + 16 * i + 8 * g);
+        u16x8_t lv = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (has_lo) lv = *reinterpret_cast<const u16x8_t*>(olo + 16 * i + 8 * g);
         const u16x8_t dv = __builtin_bit_cast(u16x8_t, doreg[i]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) del = fmaf(bf16_to_f32(ov[j]), bf16_to_f32(dv[j]), del);
+        for (int j = 0; j < 8; ++j) del = fmaf(bf16_to_f32(ov[j]) + bf16_to_f32(lv[j]), bf16_to_f32(dv[j]), del);
       }
       del += __shfl_xor(del, 32, 64);
     }
@@ -932,8 +973,8 @@ void dispatch_generic(const AttnArgs<T>& a, hipStream_t st, bool fwd) {
 }  // namespace
 
 extern "C" int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, const void* q,
-                           const void* k, const void* v, int64_t ld_qkv, void* o, int64_t ld_o, float* lse,
-                           float scale, int causal, void* stream) {
+                           const void* k, const void* v, int64_t ld_qkv, void* o, void* o_lo, int64_t ld_o,
+                           float* lse, float scale, int causal, void* stream) {
   int rc = check_common(dtype, batch, seq, heads, head_dim);
   if (rc) return rc;
   if (batch == 0 || seq == 0 || heads == 0) return RH_OK;
@@ -941,10 +982,11 @@ extern "C" int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
   RH_REQUIRE(ld_qkv >= heads * head_dim && ld_o >= heads * head_dim, "rh_attn_fwd: leading dimension too small");
   RH_REQUIRE(scale > 0.f, "rh_attn_fwd: scale must be positive (got %g)", (double)scale);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (mfma_ok(dtype, head_dim, {q, k, v, o}, {ld_qkv, ld_o})) {
+  if (dtype != RH_DTYPE_BF16) o_lo = nullptr;  // fp32 outputs are not rounded
+  if (mfma_ok(dtype, head_dim, {q, k, v, o, o_lo ? o_lo : o}, {ld_qkv, ld_o})) {
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.ld_qkv = ld_qkv;
-    a.o_out = (bf16_t*)o; a.ld_o = ld_o; a.lse_out = lse;
+    a.o_out = (bf16_t*)o; a.o_lo_out = (bf16_t*)o_lo; a.ld_o = ld_o; a.lse_out = lse;
     const int nitems = mfma_items(batch, seq, heads);
     dim3 grid((unsigned)((nitems + 1) / 2));
     if (head_dim == 64) hipLaunchKernelGGL(attn_fwd_mfma<64>, grid, dim3(512), 0, st, a, nitems);
@@ -954,7 +996,7 @@ extern "C" int rh_attn_fwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
   if (dtype == RH_DTYPE_BF16) {
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.ld_qkv = ld_qkv;
-    a.o_out = (bf16_t*)o; a.ld_o = ld_o; a.lse_out = lse;
+    a.o_out = (bf16_t*)o; a.o_lo_out = (bf16_t*)o_lo; a.ld_o = ld_o; a.lse_out = lse;
     dispatch_generic(a, st, true);
   } else {
     AttnArgs<float> a = make_args<float>(batch, seq, heads, head_dim, scale, causal);
@@ -972,7 +1014,7 @@ extern "C" int rh_attn_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t h
 }
 
 extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, const void* q,
-                           const void* k, const void* v, int64_t ld_qkv, const void* o, int64_t ld_o,
+                           const void* k, const void* v, int64_t ld_qkv, const void* o, const void* o_lo, int64_t ld_o,
                            const void* dout, int64_t ld_do, const float* lse, void* dq, void* dk, void* dv,
                            int64_t ld_dqkv, float scale, int causal, void* workspace, int64_t workspace_bytes,
                            void* stream) {
@@ -993,10 +1035,10 @@ extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
   if (dtype == RH_DTYPE_BF16) {
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.ld_qkv = ld_qkv;
-    a.o = (const bf16_t*)o; a.ld_o = ld_o; a.dout = (const bf16_t*)dout; a.ld_do = ld_do;
+    a.o = (const bf16_t*)o; a.o_lo = (const bf16_t*)o_lo; a.ld_o = ld_o; a.dout = (const bf16_t*)dout; a.ld_do = ld_do;
     a.lse = lse; a.delta = delta; a.delta_out = delta;
     a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv; a.ld_d = ld_dqkv;
-    if (mfma_ok(dtype, head_dim, {q, k, v, o, dout, dq, dk, dv}, {ld_qkv, ld_o, ld_do, ld_dqkv})) {
+    if (mfma_ok(dtype, head_dim, {q, k, v, o, o_lo ? o_lo : o, dout, dq, dk, dv}, {ld_qkv, ld_o, ld_do, ld_dqkv})) {
       // the dQ kernel also writes delta, which the dK/dV kernel reads
       const int nitems = mfma_items(batch, seq, heads);
       dim3 grid((unsigned)((nitems + 1) / 2));

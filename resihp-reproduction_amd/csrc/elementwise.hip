@@ -73,6 +73,69 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(int64_t n, T* p, const 
   }
 }
 
+// torch.optim.AdamW over many tensors in one launch.  Every workgroup takes one chunk of one
+// tensor (block ranges per tensor in `block_end`), reads the tensor's device step count (already
+// incremented by adamw_step_increment) and forms the bias corrections as torch does, in double
+// precision, rounding to fp32 where torch's scalar arguments are.
+constexpr int kMultiMax = 64;       // tensors per launch (the argument block stays under 4 KB)
+constexpr int kMultiChunk = 8192;   // elements per workgroup
+
+template <typename T>
+struct AdamMultiArgs {
+  T* p[kMultiMax];
+  const T* g[kMultiMax];
+  T* m[kMultiMax];
+  T* v[kMultiMax];
+  const float* step[kMultiMax];
+  int64_t n[kMultiMax];
+  int block_end[kMultiMax];
+  int count;
+  double lr, b1, b2, eps, wd;
+};
+
+__global__ __launch_bounds__(64) void adamw_step_increment(AdamMultiArgs<float> a) {
+  if ((int)threadIdx.x < a.count) {
+    float* s = const_cast<float*>(a.step[threadIdx.x]);
+    *s = *s + 1.0f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void adamw_update(T* p, const T* g, T* m, T* v, float decay, float omb1, float b2f,
+                                             float omb2, float step_size, float bc2_sqrt, float eps) {
+  float w = ld_f32(p) * decay;
+  const float gr = ld_f32(g);
+  float mv = ld_f32(m);
+  mv = mv + (gr - mv) * omb1;
+  const float vv = ld_f32(v) * b2f + omb2 * gr * gr;
+  st_f32(m, mv);
+  st_f32(v, vv);
+  const float mq = ld_f32(m), vq = ld_f32(v);  // the stored (rounded) moments, as torch uses them
+  w = w - step_size * (mq / (sqrtf(vq) / bc2_sqrt + eps));
+  st_f32(p, w);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void adamw_multi_kernel(AdamMultiArgs<T> a) {
+  const int b = blockIdx.x;
+  int t = 0;
+  while (t + 1 < a.count && a.block_end[t] <= b) ++t;
+  const int first = t ? a.block_end[t - 1] : 0;
+  const int64_t lo = (int64_t)(b - first) * kMultiChunk;
+  const int64_t hi = min(a.n[t], lo + kMultiChunk);
+  const double s = (double)*a.step[t];
+  const float step_size = (float)(a.lr / (1.0 - pow(a.b1, s)));
+  const float bc2_sqrt = (float)sqrt(1.0 - pow(a.b2, s));
+  const float decay = (float)(1.0 - a.lr * a.wd);
+  const float omb1 = (float)(1.0 - a.b1), b2f = (float)a.b2, omb2 = (float)(1.0 - a.b2), eps = (float)a.eps;
+  T* p = a.p[t];
+  const T* g = a.g[t];
+  T* m = a.m[t];
+  T* v = a.v[t];
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads)
+    adamw_update(p + i, g + i, m + i, v + i, decay, omb1, b2f, omb2, step_size, bc2_sqrt, eps);
+}
+
 int check_dtype(int dtype, const char* who) {
   if (dtype != RH_DTYPE_F32 && dtype != RH_DTYPE_BF16) return rh_set_error(RH_ERR_INVALID, "%s: unknown dtype %d", who, dtype);
   return RH_OK;
@@ -179,4 +242,62 @@ extern "C" int rh_adamw_step(int dtype, int64_t n, void* param, const void* grad
                        (const float*)grad, (float*)exp_avg, (float*)exp_avg_sq, lr, beta1, beta2, eps, weight_decay,
                        bias_c1, bc2s);
   return rh_check_launch("rh_adamw_step");
+}
+
+extern "C" int rh_adamw_multi(int dtype, int n_tensors, const rh_adamw_tensor* tensors, double lr, double beta1,
+                              double beta2, double eps, double weight_decay, void* stream) {
+  int rc = check_dtype(dtype, "rh_adamw_multi");
+  if (rc) return rc;
+  RH_REQUIRE(n_tensors >= 0, "rh_adamw_multi: negative tensor count");
+  if (n_tensors == 0) return RH_OK;
+  RH_REQUIRE(tensors != nullptr, "rh_adamw_multi: null tensor list");
+  RH_REQUIRE(lr >= 0 && eps >= 0 && weight_decay >= 0 && beta1 >= 0 && beta1 < 1 && beta2 >= 0 && beta2 < 1,
+             "rh_adamw_multi: invalid hyperparameters");
+  for (int i = 0; i < n_tensors; ++i) {
+    const rh_adamw_tensor& t = tensors[i];
+    RH_REQUIRE(t.numel >= 0, "rh_adamw_multi: tensor %d has a negative size", i);
+    RH_REQUIRE(t.numel == 0 || (t.param && t.grad && t.exp_avg && t.exp_avg_sq), "rh_adamw_multi: tensor %d: null pointer", i);
+    RH_REQUIRE(t.step, "rh_adamw_multi: tensor %d: null step counter", i);
+    for (int j = 0; j < i; ++j)
+      RH_REQUIRE(tensors[j].step != t.step, "rh_adamw_multi: tensors %d and %d share a step counter", j, i);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int base = 0; base < n_tensors; base += kMultiMax) {
+    const int cnt = min(kMultiMax, n_tensors - base);
+    AdamMultiArgs<float> a{};  // pointers are reinterpreted per dtype below; the layout is identical
+    int64_t blocks = 0;
+    for (int i = 0; i < cnt; ++i) {
+      const rh_adamw_tensor& t = tensors[base + i];
+      a.p[i] = (float*)t.param;
+      a.g[i] = (const float*)t.grad;
+      a.m[i] = (float*)t.exp_avg;
+      a.v[i] = (float*)t.exp_avg_sq;
+      a.step[i] = t.step;
+      a.n[i] = t.numel;
+      blocks += rh_cdiv(t.numel, kMultiChunk);
+      RH_REQUIRE(blocks <= INT32_MAX, "rh_adamw_multi: too many elements in one launch");
+      a.block_end[i] = (int)blocks;
+    }
+    a.count = cnt;
+    a.lr = lr;
+    a.b1 = beta1;
+    a.b2 = beta2;
+    a.eps = eps;
+    a.wd = weight_decay;
+    hipLaunchKernelGGL(adamw_step_increment, dim3(1), dim3(64), 0, st, a);
+    rc = rh_check_launch("rh_adamw_multi (step count)");
+    if (rc) return rc;
+    if (blocks == 0) continue;
+    if (dtype == RH_DTYPE_BF16) {
+      AdamMultiArgs<bf16_t> ab;
+      static_assert(sizeof(ab) == sizeof(a), "argument layouts must match");
+      __builtin_memcpy(&ab, &a, sizeof(a));
+      hipLaunchKernelGGL(adamw_multi_kernel<bf16_t>, dim3((unsigned)blocks), dim3(kThreads), 0, st, ab);
+    } else {
+      hipLaunchKernelGGL(adamw_multi_kernel<float>, dim3((unsigned)blocks), dim3(kThreads), 0, st, a);
+    }
+    rc = rh_check_launch("rh_adamw_multi");
+    if (rc) return rc;
+  }
+  return RH_OK;
 }

@@ -4,17 +4,27 @@
 // Ids outside this rank's vocabulary slice give a zero row (vocab-parallel
 // lookup).
 //
-// Backward: the (id, token position) pairs are sorted once in LDS by a
-// single-block bitonic sort (keys id<<32 | position, so equal ids keep
-// ascending position order), then one wavefront per distinct id sums the
-// gradient rows of that id in position order and adds the sum to its
-// embedding-gradient row.  No atomics: the result is bit-reproducible.
+// Backward, for any token count: the (id, token position) pairs are sorted by a
+// bitonic network over keys id<<32 | position (so equal ids keep ascending position
+// order) -- compare distances below 8192 run inside one workgroup's LDS tile, larger
+// ones as global passes -- and the gradient rows are then summed per id in two levels:
+//   1. the sorted rows are cut into chunks of 32; each workgroup sums every id's rows
+//      inside its chunk in position order.  An id whose rows all lie in the chunk is
+//      added to its embedding-gradient row at once; the piece of an id that continues
+//      into a neighbouring chunk goes to an fp32 slot of the workspace;
+//   2. for every id spanning several chunks, one workgroup adds its pieces in chunk
+//      order and adds the sum to the gradient row.
+// A heavily repeated id therefore costs one chunk-parallel pass plus a walk over its
+// chunk pieces rather than a serial pass over its rows.  No atomics: the summation
+// order depends only on the sorted keys, so the result is bit-reproducible.
 // The position gradient is a per-(position, column) sum over the batch.
 #include "common.hpp"
 
 namespace {
 
-constexpr int kSortMax = 16384;  // tokens per call for the LDS sort (128 KiB of keys)
+constexpr int kTile = 8192;   // keys per LDS tile of the bitonic sort (64 KiB)
+constexpr int kChunk = 32;    // sorted rows per workgroup of the segmented sum
+constexpr uint64_t kNoKey = ~0ull;
 
 template <typename T>
 __global__ __launch_bounds__(256) void emb_fwd_kernel(int64_t rows, int S, int dim, const int64_t* __restrict__ tok,
@@ -59,35 +69,57 @@ __global__ __launch_bounds__(256) void emb_fwd_kernel(int64_t rows, int S, int d
   }
 }
 
-__global__ __launch_bounds__(1024) void emb_sort_kernel(int64_t n, const int64_t* __restrict__ tok, int64_t vstart,
-                                                          int64_t vrows, int N, uint64_t* __restrict__ keys) {
-  __shared__ uint64_t sk[kSortMax];
-  for (int i = threadIdx.x; i < N; i += 1024) {
-    uint64_t key = ~0ull;
+// keys[i] = local id << 32 | i for the n token positions (kNoKey for ids outside the slice and
+// for the padding up to the power of two N)
+__global__ __launch_bounds__(256) void emb_keys_kernel(int64_t n, int64_t N, const int64_t* __restrict__ tok,
+                                                        int64_t vstart, int64_t vrows, uint64_t* __restrict__ keys) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256) {
+    uint64_t key = kNoKey;
     if (i < n) {
       const int64_t local = tok[i] - vstart;
       if (local >= 0 && local < vrows) key = ((uint64_t)local << 32) | (uint64_t)i;
     }
-    sk[i] = key;
+    keys[i] = key;
   }
+}
+
+// Bitonic stages k in [k_lo, k_hi] (powers of two), each with every compare distance
+// j < min(k, tile), on one LDS tile of `tile` keys per workgroup.  Pair (i, i ^ j) is put in
+// ascending order when bit k of the global index i is clear, descending otherwise.
+__global__ __launch_bounds__(1024) void emb_bitonic_tile(uint64_t* __restrict__ keys, int tile, int64_t k_lo,
+                                                          int64_t k_hi) {
+  __shared__ uint64_t sk[kTile];
+  const int64_t base = (int64_t)blockIdx.x * tile;
+  for (int i = threadIdx.x; i < tile; i += 1024) sk[i] = keys[base + i];
   __syncthreads();
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < N; i += 1024) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t a = sk[i], b = sk[ixj];
-          const bool up = (i & k) == 0;
-          if (up ? (a > b) : (a < b)) {
-            sk[i] = b;
-            sk[ixj] = a;
-          }
+  for (int64_t k = k_lo; k <= k_hi; k <<= 1) {
+    for (int j = (int)min<int64_t>(k, tile) >> 1; j > 0; j >>= 1) {
+      for (int t = threadIdx.x; t < tile / 2; t += 1024) {
+        const int i = (t / j) * 2 * j + (t % j);  // i has bit j clear; its partner is i + j
+        const uint64_t a = sk[i], b = sk[i + j];
+        const bool up = ((base + i) & k) == 0;
+        if (up ? (a > b) : (a < b)) {
+          sk[i] = b;
+          sk[i + j] = a;
         }
       }
       __syncthreads();
     }
   }
-  for (int i = threadIdx.x; i < n; i += 1024) keys[i] = sk[i];
+  for (int i = threadIdx.x; i < tile; i += 1024) keys[base + i] = sk[i];
+}
+
+// One bitonic compare distance j >= tile of stage k, over global memory.
+__global__ __launch_bounds__(256) void emb_bitonic_global(uint64_t* __restrict__ keys, int64_t N, int64_t k, int64_t j) {
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < N / 2; t += (int64_t)gridDim.x * 256) {
+    const int64_t i = (t / j) * 2 * j + (t % j);
+    const uint64_t a = keys[i], b = keys[i + j];
+    const bool up = (i & k) == 0;
+    if (up ? (a > b) : (a < b)) {
+      keys[i] = b;
+      keys[i + j] = a;
+    }
+  }
 }
 
 template <typename T>
@@ -95,25 +127,97 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(int64_t n, T* p) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) st_f32(p + i, 0.f);
 }
 
+__device__ __forceinline__ uint64_t key_id(uint64_t k) { return k >> 32; }
+
+// Level 1 of the per-id sum: workgroup c sums the sorted rows [32c, 32c + 32) per id, each
+// thread over its own columns (all 32 row loads of a column issued before the sums).  Piece
+// slots: head[c] holds the chunk's first piece when that id began in an earlier chunk; tail[c]
+// its last piece when that id continues into the next chunk and began in this one.  Pieces
+// closed on both sides go straight into dW.
 template <typename T>
-__global__ __launch_bounds__(256) void emb_seg_kernel(int64_t n, int dim, const uint64_t* __restrict__ keys,
-                                                       const T* __restrict__ dout, T* __restrict__ dW) {
-  const int lane = threadIdx.x & 63;
-  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (i >= n) return;
-  const uint64_t k = keys[i];
-  if (k == ~0ull) return;
-  const uint64_t id = k >> 32;
-  if (i > 0 && (keys[i - 1] >> 32) == id) return;  // not the first row of this id
-  T* w = dW + (int64_t)id * dim;
-  for (int c = lane; c < dim; c += 64) {
-    float acc = 0.f;
-    for (int64_t j = i; j < n; ++j) {
-      const uint64_t kj = keys[j];
-      if ((kj >> 32) != id) break;
-      acc += ld_f32(dout + (int64_t)(kj & 0xffffffffu) * dim + c);
+__global__ __launch_bounds__(256) void emb_chunk_sum(int64_t n, int dim, const uint64_t* __restrict__ keys,
+                                                      const T* __restrict__ dout, T* __restrict__ dW,
+                                                      float* __restrict__ head, float* __restrict__ tail) {
+  __shared__ uint64_t sk[kChunk + 2];  // keys of rows lo-1 .. hi (kNoKey outside [0, n))
+  const int64_t c = blockIdx.x;
+  const int64_t lo = c * kChunk;
+  const int m = (int)min<int64_t>(kChunk, n - lo);
+  if (threadIdx.x < kChunk + 2) {
+    const int64_t r = lo - 1 + threadIdx.x;
+    sk[threadIdx.x] = (r >= 0 && r < n) ? keys[r] : kNoKey;
+  }
+  __syncthreads();
+  if (sk[1] == kNoKey) return;
+  for (int col = threadIdx.x; col < dim; col += 256) {
+    float val[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const uint64_t k = sk[i + 1];
+      val[i] = (i < m && k != kNoKey) ? ld_f32(dout + (int64_t)(k & 0xffffffffu) * dim + col) : 0.f;
     }
-    st_f32(w + c, ld_f32(w + c) + acc);
+    float acc = 0.f;
+    bool first_piece = true;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const uint64_t k = sk[i + 1];
+      if (i >= m || k == kNoKey) break;
+      acc += val[i];
+      const uint64_t next = sk[i + 2];  // row lo + i + 1 (the next chunk's first row when i = m - 1)
+      const bool same_next = next != kNoKey && key_id(next) == key_id(k);
+      if (same_next && i + 1 < m) continue;  // the id goes on inside this chunk
+      const bool open_start = first_piece && sk[0] != kNoKey && key_id(sk[0]) == key_id(k);
+      if (open_start) {
+        head[c * dim + col] = acc;
+      } else if (same_next) {
+        tail[c * dim + col] = acc;
+      } else {
+        T* w = dW + (int64_t)key_id(k) * dim + col;
+        st_f32(w, ld_f32(w) + acc);
+      }
+      acc = 0.f;
+      first_piece = false;
+    }
+  }
+}
+
+// Level 2: an id that begins in chunk c and continues past it sums tail[c] and the head slots
+// of the following chunks it covers, then adds the sum to its gradient row.  Its last row is
+// found by a binary search of the sorted keys; workgroup (c, y) covers columns 64y .. 64y+63,
+// wave w sums pieces w, w+4, ... in order and the four wave sums are added in wave order.
+template <typename T>
+__global__ __launch_bounds__(256) void emb_chunk_join(int64_t n, int dim, const uint64_t* __restrict__ keys,
+                                                       T* __restrict__ dW, const float* __restrict__ head,
+                                                       const float* __restrict__ tail) {
+  __shared__ float part[4][64];
+  const int64_t c = blockIdx.x;
+  const int64_t lo = c * kChunk;
+  const int64_t last = min(n, lo + kChunk) - 1;  // last row of chunk c
+  if (last + 1 >= n) return;
+  const uint64_t k = keys[last], nk = keys[last + 1];
+  if (k == kNoKey || nk == kNoKey || key_id(nk) != key_id(k)) return;  // nothing continues
+  const uint64_t id = key_id(k);
+  // a chunk holding only this id, which also began before it, is a middle piece (head slot)
+  if (key_id(keys[lo]) == id && lo > 0 && key_id(keys[lo - 1]) == id) return;
+  int64_t a = last + 1, b = n;  // first row past this id: keys are sorted, kNoKey last
+  while (a < b) {
+    const int64_t mid = (a + b) / 2;
+    const uint64_t km = keys[mid];
+    if (km != kNoKey && key_id(km) == id) a = mid + 1;
+    else b = mid;
+  }
+  const int64_t pieces = (a - 1) / kChunk - c + 1;  // tail[c], head[c + 1 .. (a - 1) / 32]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = blockIdx.y * 64 + lane;
+  float acc = 0.f;
+  if (col < dim) {
+    for (int64_t q = wave; q < pieces; q += 4) acc += q == 0 ? tail[c * dim + col] : head[(c + q) * dim + col];
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && col < dim) {
+    const float sum = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    T* w = dW + (int64_t)id * dim + col;
+    st_f32(w, ld_f32(w) + sum);
   }
 }
 
@@ -157,9 +261,19 @@ extern "C" int rh_embedding_fwd(int dtype, int64_t batch, int64_t seq, int64_t d
   return rh_check_launch("rh_embedding_fwd");
 }
 
-extern "C" int rh_embedding_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t* bytes) {
-  RH_REQUIRE(bytes && batch >= 0 && seq >= 0, "rh_embedding_bwd_workspace_bytes: bad arguments");
-  *bytes = batch * seq * (int64_t)sizeof(uint64_t);
+// sort keys (next power of two >= tokens) + head and tail piece slots of every 32-row chunk
+static int64_t emb_ws_layout(int64_t rows, int64_t dim, int64_t* N_out, int64_t* chunks_out) {
+  int64_t N = 1;
+  while (N < rows) N <<= 1;
+  const int64_t chunks = rh_cdiv(rows, kChunk);
+  if (N_out) *N_out = N;
+  if (chunks_out) *chunks_out = chunks;
+  return N * (int64_t)sizeof(uint64_t) + 2 * chunks * dim * (int64_t)sizeof(float);
+}
+
+extern "C" int rh_embedding_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t dim, int64_t* bytes) {
+  RH_REQUIRE(bytes && batch >= 0 && seq >= 0 && dim >= 0, "rh_embedding_bwd_workspace_bytes: bad arguments");
+  *bytes = batch * seq == 0 ? 0 : emb_ws_layout(batch * seq, dim, nullptr, nullptr);
   return RH_OK;
 }
 
@@ -182,18 +296,41 @@ extern "C" int rh_embedding_bwd(int dtype, int64_t batch, int64_t seq, int64_t d
     }
     if (rows > 0) {
       RH_REQUIRE(tokens && dout, "rh_embedding_bwd: null pointer");
-      RH_REQUIRE(rows <= kSortMax, "rh_embedding_bwd: %lld tokens per call exceeds %d", (long long)rows, kSortMax);
-      RH_REQUIRE(workspace && workspace_bytes >= rows * (int64_t)sizeof(uint64_t),
-                 "rh_embedding_bwd: workspace of %lld bytes is too small", (long long)workspace_bytes);
-      int N = 1;
-      while (N < rows) N <<= 1;
+      RH_REQUIRE(rows < (1ll << 31), "rh_embedding_bwd: %lld tokens per call exceeds 2^31 - 1", (long long)rows);
+      int64_t N = 0, chunks = 0;
+      const int64_t need = emb_ws_layout(rows, dim, &N, &chunks);
+      RH_REQUIRE(workspace && workspace_bytes >= need && rh_aligned(workspace, 16),
+                 "rh_embedding_bwd: workspace of %lld bytes is too small (%lld needed, 16-byte aligned)",
+                 (long long)workspace_bytes, (long long)need);
       uint64_t* keys = static_cast<uint64_t*>(workspace);
-      hipLaunchKernelGGL(emb_sort_kernel, dim3(1), dim3(1024), 0, st, rows, tokens, vocab_start, vocab_rows, N, keys);
-      const unsigned g = (unsigned)rh_cdiv(rows, 4);
-      if (bf16) hipLaunchKernelGGL(emb_seg_kernel<bf16_t>, dim3(g), dim3(256), 0, st, rows, (int)dim, keys,
-                                   (const bf16_t*)dout, (bf16_t*)dtok);
-      else hipLaunchKernelGGL(emb_seg_kernel<float>, dim3(g), dim3(256), 0, st, rows, (int)dim, keys,
-                              (const float*)dout, (float*)dtok);
+      float* head = reinterpret_cast<float*>(keys + N);
+      float* tail = head + chunks * dim;
+      const unsigned gk = (unsigned)std::min<int64_t>(rh_cdiv(N, 256), 65536);
+      hipLaunchKernelGGL(emb_keys_kernel, dim3(gk), dim3(256), 0, st, rows, N, tokens, vocab_start, vocab_rows, keys);
+      // bitonic sort: stages up to the tile size inside LDS, then per larger stage the global
+      // compare distances down to the tile size and one LDS launch for the rest
+      const int tile = (int)std::min<int64_t>(N, kTile);
+      const unsigned tiles = (unsigned)(N / tile);
+      hipLaunchKernelGGL(emb_bitonic_tile, dim3(tiles), dim3(1024), 0, st, keys, tile, (int64_t)2, (int64_t)tile);
+      const unsigned gg = (unsigned)std::min<int64_t>(rh_cdiv(N / 2, 256), 65536);
+      for (int64_t k = 2 * (int64_t)tile; k <= N; k <<= 1) {
+        for (int64_t j = k >> 1; j >= tile; j >>= 1)
+          hipLaunchKernelGGL(emb_bitonic_global, dim3(gg), dim3(256), 0, st, keys, N, k, j);
+        hipLaunchKernelGGL(emb_bitonic_tile, dim3(tiles), dim3(1024), 0, st, keys, tile, k, k);
+      }
+      const unsigned gc = (unsigned)chunks;
+      const dim3 gj((unsigned)chunks, (unsigned)rh_cdiv(dim, 64));
+      if (bf16) {
+        hipLaunchKernelGGL(emb_chunk_sum<bf16_t>, dim3(gc), dim3(256), 0, st, rows, (int)dim, keys,
+                           (const bf16_t*)dout, (bf16_t*)dtok, head, tail);
+        hipLaunchKernelGGL(emb_chunk_join<bf16_t>, gj, dim3(256), 0, st, rows, (int)dim, keys, (bf16_t*)dtok,
+                           head, tail);
+      } else {
+        hipLaunchKernelGGL(emb_chunk_sum<float>, dim3(gc), dim3(256), 0, st, rows, (int)dim, keys,
+                           (const float*)dout, (float*)dtok, head, tail);
+        hipLaunchKernelGGL(emb_chunk_join<float>, gj, dim3(256), 0, st, rows, (int)dim, keys, (float*)dtok, head,
+                           tail);
+      }
     }
     rc = rh_check_launch("rh_embedding_bwd (token)");
     if (rc) return rc;

@@ -94,9 +94,8 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
     return RH_OK;
   }
   const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
-  static const int waves[4][2] = {{2, 4}, {4, 2}, {2, 2}, {4, 2}};
   snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma_ok(desc, pl, p) ? "gemm_bf16_dma" : "gemm_bf16_mfma",
-           kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, waves[pl.cfg][0], waves[pl.cfg][1], desc->layout,
+           kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, kWaves[pl.cfg][0], kWaves[pl.cfg][1], desc->layout,
            pl.splits + pl.tail > 1 ? 0 : desc->epilogue,  // split slices use the RH_EPI_NONE kernels
            split);
   return RH_OK;

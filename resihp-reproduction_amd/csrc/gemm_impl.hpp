@@ -946,6 +946,8 @@ struct TileShape {
   int bm, bn, threads;
 };
 constexpr TileShape kShapes[5] = {{256, 256, 512}, {256, 128, 512}, {128, 128, 256}, {256, 192, 512}, {fBM, fBN, 256}};
+// waves (rows x columns) of each bf16 tile shape
+constexpr int kWaves[5][2] = {{2, 4}, {4, 2}, {2, 2}, {4, 2}, {0, 0}};
 
 struct Plan {
   int cfg;
@@ -991,6 +993,7 @@ inline Plan plan_gemm(const rh_gemm_desc* d) {
   double best = 1e300;
   for (int c = 0; c < 4; ++c) {
     if (only >= 0 && c != only) continue;
+    const double eff = kTileEff[c];
     if (c == kT256x192 && d->layout != RH_GEMM_NT) continue;
     const int64_t tm = rh_cdiv(d->M, kShapes[c].bm), tn = rh_cdiv(d->N, kShapes[c].bn);
     const int64_t tiles = tm * tn;
@@ -1000,7 +1003,7 @@ inline Plan plan_gemm(const rh_gemm_desc* d) {
       if (splits > 1 && (Kp / splits < 512 || tiles * (splits - 1) >= slots)) break;
       const int64_t kps = rh_cdiv(rh_cdiv(Kp, splits), kBK) * kBK;
       const int64_t waves = rh_cdiv(tiles * splits, slots);
-      double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / kTileEff[c];
+      double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / eff;
       // partial write + reduce: measured on MI355X, a split-4 2048x2048 reduce costs ~1/4 of a
       // 256x256x2048 tile wave, i.e. ~2 units per partial element
       if (splits > 1) t += 2.0 * (double)splits * d->M * d->N;

@@ -85,6 +85,17 @@ class rh_copy2d(ctypes.Structure):
     ]
 
 
+class rh_adamw_tensor(ctypes.Structure):
+    _fields_ = [
+        ("param", c_ptr),
+        ("grad", c_ptr),
+        ("exp_avg", c_ptr),
+        ("exp_avg_sq", c_ptr),
+        ("step", c_ptr),
+        ("numel", c_i64),
+    ]
+
+
 # name -> argtypes (every function returns int, except rh_last_error)
 _SIGNATURES = {
     "rh_version": [],
@@ -92,10 +103,10 @@ _SIGNATURES = {
     "rh_gemm": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_ptr],
     "rh_gemm_stage": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_int, c_ptr],
     "rh_gemm_kernel_name": [ctypes.POINTER(rh_gemm_desc), ctypes.c_char_p, c_i64],
-    "rh_attn_fwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_float,
-                    c_int, c_ptr],
+    "rh_attn_fwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr,
+                    c_float, c_int, c_ptr],
     "rh_attn_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],
-    "rh_attn_bwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64,
+    "rh_attn_bwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                     c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_float, c_int, c_ptr, c_i64, c_ptr],
     "rh_layernorm_fwd": [c_int, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_float, c_ptr, c_ptr, c_ptr, c_ptr],
     "rh_layernorm_bwd_workspace_bytes": [c_i64, c_i64, ctypes.POINTER(c_i64)],
@@ -108,12 +119,14 @@ _SIGNATURES = {
     "rh_sgd_step": [c_int, c_i64, c_ptr, c_ptr, c_float, c_float, c_ptr],
     "rh_adamw_step": [c_int, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_float, c_float, c_float, c_float, c_float, c_float,
                       c_float, c_ptr],
+    "rh_adamw_multi": [c_int, c_int, ctypes.POINTER(rh_adamw_tensor), ctypes.c_double, ctypes.c_double,
+                       ctypes.c_double, ctypes.c_double, ctypes.c_double, c_ptr],
     "rh_xent_workspace_bytes": [c_i64, c_i64, ctypes.POINTER(c_i64)],
     "rh_xent_fwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                     c_ptr],
     "rh_xent_bwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr],
     "rh_embedding_fwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
-    "rh_embedding_bwd_workspace_bytes": [c_i64, c_i64, ctypes.POINTER(c_i64)],
+    "rh_embedding_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],
     "rh_embedding_bwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_int, c_ptr, c_i64,
                          c_ptr],
     "rh_copy2d_batch": [ctypes.POINTER(rh_copy2d), c_int, c_ptr],

@@ -127,7 +127,10 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
         with profiling.launch(name.value.decode(), 2.0 * M * N * K):
             H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_MAIN, H.stream_of(A))
         if nbytes:
-            with profiling.launch("gemm_splitk_reduce", 0.0):
+            # fp32 partials read once; D written, C / aux read or written once (2-byte bf16 storage)
+            es = A.element_size()
+            io = 1 + (beta != 0.0) + (epilogue != H.RH_EPI_NONE)
+            with profiling.launch("gemm_splitk_reduce", 0.0, nbytes + io * M * N * es):
                 H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_REDUCE,
                        H.stream_of(A))
         return
@@ -216,8 +219,10 @@ def ln_fwd(x2: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float):
     mean = torch.empty(rows, dtype=torch.float32, device=x2.device)
     rstd = torch.empty(rows, dtype=torch.float32, device=x2.device)
     H.require_gpu(x2, w, b)
-    H.call("rh_layernorm_fwd", _same_dtype(x2, w, b), rows, dim, x2.data_ptr(), w.data_ptr(), b.data_ptr(),
-           float(eps), y.data_ptr(), mean.data_ptr(), rstd.data_ptr(), H.stream_of(x2))
+    es = x2.element_size()
+    with profiling.launch("ln_fwd", 0.0, 2 * rows * dim * es + 8 * rows + 2 * dim * es):
+        H.call("rh_layernorm_fwd", _same_dtype(x2, w, b), rows, dim, x2.data_ptr(), w.data_ptr(), b.data_ptr(),
+               float(eps), y.data_ptr(), mean.data_ptr(), rstd.data_ptr(), H.stream_of(x2))
     return y, mean, rstd
 
 
@@ -244,9 +249,13 @@ def ln_bwd(dy2: torch.Tensor, x2: torch.Tensor, mean: torch.Tensor, rstd: torch.
     gb = gb_t[0] if gb_t else None
     nbytes = H.query("rh_layernorm_bwd_workspace_bytes", rows, dim)
     ws = H.workspace(nbytes, dev)
-    H.call("rh_layernorm_bwd", _same_dtype(dy2, x2, w, dres), rows, dim, dy2.data_ptr(), x2.data_ptr(),
-           mean.data_ptr(), rstd.data_ptr(), w.data_ptr(), H.ptr(dres), dx.data_ptr(), H.ptr(gw), H.ptr(gb),
-           1 if acc else 0, H.ptr(ws), nbytes, H.stream_of(x2))
+    # dy, x, (dres) read and dx written once; mean/rstd read; dgamma/dbeta written (and read when accumulating)
+    es = x2.element_size()
+    moved = (3 + (dres is not None)) * rows * dim * es + 8 * rows + len(present) * dim * es * (2 if acc else 1)
+    with profiling.launch("ln_bwd (+ column sums)", 0.0, moved):
+        H.call("rh_layernorm_bwd", _same_dtype(dy2, x2, w, dres), rows, dim, dy2.data_ptr(), x2.data_ptr(),
+               mean.data_ptr(), rstd.data_ptr(), w.data_ptr(), H.ptr(dres), dx.data_ptr(), H.ptr(gw), H.ptr(gb),
+               1 if acc else 0, H.ptr(ws), nbytes, H.stream_of(x2))
     if gw is not None:
         _finish_grad(w, gw)
     if gb is not None:
@@ -258,16 +267,21 @@ def ln_bwd(dy2: torch.Tensor, x2: torch.Tensor, mean: torch.Tensor, rstd: torch.
 # attention core
 # ---------------------------------------------------------------------------
 def attn_fwd(qkv: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int):
-    """qkv [T, 3*d_l] (q | k | v) -> context [T, d_l], lse [batch, heads, seq]."""
+    """qkv [T, 3*d_l] (q | k | v) -> context [T, d_l], lse [batch, heads, seq] and, for bf16, the
+    context's rounding residual [T, d_l] (context - bf16(context)), which the backward needs to form
+    delta = do . o from the unrounded output (None for fp32)."""
     dl = heads * head_dim
     T = qkv.shape[0]
     ctx = torch.empty((T, dl), dtype=qkv.dtype, device=qkv.device)
+    ctx_lo = torch.empty((T, dl), dtype=qkv.dtype, device=qkv.device) if qkv.dtype == torch.bfloat16 else None
     lse = torch.empty((batch, heads, seq), dtype=torch.float32, device=qkv.device)
     es = qkv.element_size()
     base = qkv.data_ptr()
     with profiling.launch(f"attn_fwd_mfma<{head_dim}>", attn_flops(batch, seq, heads, head_dim)):
-        _attn_fwd_call(qkv, batch, seq, heads, head_dim, dl, es, base, ctx, lse)
-    return ctx, lse
+        H.call("rh_attn_fwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es,
+               base + 2 * dl * es, _ld(qkv), ctx.data_ptr(), H.ptr(ctx_lo), dl, lse.data_ptr(),
+               1.0 / math.sqrt(head_dim), 1, H.stream_of(qkv))
+    return ctx, lse, ctx_lo
 
 
 def attn_flops(batch: int, seq: int, heads: int, head_dim: int) -> float:
@@ -275,13 +289,8 @@ def attn_flops(batch: int, seq: int, heads: int, head_dim: int) -> float:
     return 4.0 * batch * heads * head_dim * seq * (seq + 1) / 2
 
 
-def _attn_fwd_call(qkv, batch, seq, heads, head_dim, dl, es, base, ctx, lse):
-    H.call("rh_attn_fwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es, base + 2 * dl * es,
-           _ld(qkv), ctx.data_ptr(), dl, lse.data_ptr(), 1.0 / math.sqrt(head_dim), 1, H.stream_of(qkv))
-
-
 def attn_bwd(dctx: torch.Tensor, qkv: torch.Tensor, ctx: torch.Tensor, lse: torch.Tensor, batch: int, seq: int,
-             heads: int, head_dim: int) -> torch.Tensor:
+             heads: int, head_dim: int, ctx_lo: torch.Tensor | None = None) -> torch.Tensor:
     dl = heads * head_dim
     T = qkv.shape[0]
     dctx = dctx.contiguous()
@@ -293,9 +302,9 @@ def attn_bwd(dctx: torch.Tensor, qkv: torch.Tensor, ctx: torch.Tensor, lse: torc
     with profiling.launch(f"attn_bwd_dq_mfma<{head_dim}> + attn_bwd_dkdv_mfma<{head_dim}>",
                           2.0 * attn_flops(batch, seq, heads, head_dim)):
         H.call("rh_attn_bwd", H.dtype_code(qkv), batch, seq, heads, head_dim, base, base + dl * es,
-               base + 2 * dl * es, _ld(qkv), ctx.data_ptr(), dl, dctx.data_ptr(), _ld(dctx), lse.data_ptr(), dbase,
-               dbase + dl * es, dbase + 2 * dl * es, 3 * dl, 1.0 / math.sqrt(head_dim), 1, H.ptr(ws), nbytes,
-               H.stream_of(qkv))
+               base + 2 * dl * es, _ld(qkv), ctx.data_ptr(), H.ptr(ctx_lo), dl, dctx.data_ptr(), _ld(dctx),
+               lse.data_ptr(), dbase, dbase + dl * es, dbase + 2 * dl * es, 3 * dl, 1.0 / math.sqrt(head_dim), 1,
+               H.ptr(ws), nbytes, H.stream_of(qkv))
     return dqkv
 
 
@@ -311,12 +320,12 @@ def _check_heads(width: int, num_heads: int) -> int:
 def _attention_forward(n1, wq, wk, wv, num_heads, batch, seq):
     head_dim = _check_heads(wq.shape[0], num_heads)
     qkv = linear_fwd(n1, [wq, wk, wv])
-    ctx, lse = attn_fwd(qkv, batch, seq, num_heads, head_dim)
-    return qkv, ctx, lse, head_dim
+    ctx, lse, ctx_lo = attn_fwd(qkv, batch, seq, num_heads, head_dim)
+    return qkv, ctx, lse, ctx_lo, head_dim
 
 
-def _attention_backward(dctx, n1, qkv, ctx, lse, wq, wk, wv, num_heads, head_dim, batch, seq, need_dx=True):
-    dqkv = attn_bwd(dctx, qkv, ctx, lse, batch, seq, num_heads, head_dim)
+def _attention_backward(dctx, n1, qkv, ctx, lse, ctx_lo, wq, wk, wv, num_heads, head_dim, batch, seq, need_dx=True):
+    dqkv = attn_bwd(dctx, qkv, ctx, lse, batch, seq, num_heads, head_dim, ctx_lo)
     dn1 = linear_dgrad(dqkv, [wq, wk, wv]) if need_dx else None
     linear_wgrad(dqkv, n1, [wq, wk, wv])
     return dn1
@@ -416,7 +425,7 @@ class _EmbeddingFn(torch.autograd.Function):
             if not acc_p:
                 gp.zero_()
             acc_p = True
-        nbytes = H.query("rh_embedding_bwd_workspace_bytes", batch, seq)
+        nbytes = H.query("rh_embedding_bwd_workspace_bytes", batch, seq, dim)
         ws = H.workspace(nbytes, dout.device)
         stream = H.stream_of(dout)
         if want_tok:
@@ -439,22 +448,22 @@ class _AttentionFn(torch.autograd.Function):
         H.require_gpu(x, wq, wk, wv, wo)
         batch, seq, dim = x.shape
         x2 = _as_rows(x).contiguous()
-        qkv, c, lse, head_dim = _attention_forward(x2, wq, wk, wv, num_heads, batch, seq)
+        qkv, c, lse, c_lo, head_dim = _attention_forward(x2, wq, wk, wv, num_heads, batch, seq)
         out = linear_fwd(c, [wo])
-        ctx.save_for_backward(x2, qkv, c, lse)
+        ctx.save_for_backward(x2, qkv, c, lse, c_lo)
         ctx.params = (wq, wk, wv, wo)
         ctx.meta = (batch, seq, num_heads, head_dim)
         return out.view(batch, seq, wo.shape[0])
 
     @staticmethod
     def backward(ctx, dout):
-        x2, qkv, c, lse = ctx.saved_tensors
+        x2, qkv, c, lse, c_lo = ctx.saved_tensors
         wq, wk, wv, wo = ctx.params
         batch, seq, num_heads, head_dim = ctx.meta
         dout2 = _as_rows(dout).contiguous()
         dctx = linear_dgrad(dout2, [wo])
         linear_wgrad(dout2, c, [wo])
-        dx = _attention_backward(dctx, x2, qkv, c, lse, wq, wk, wv, num_heads, head_dim, batch, seq,
+        dx = _attention_backward(dctx, x2, qkv, c, lse, c_lo, wq, wk, wv, num_heads, head_dim, batch, seq,
                                  need_dx=ctx.needs_input_grad[0])
         return (dx.view(batch, seq, -1) if dx is not None else None), None, None, None, None, None
 
@@ -504,20 +513,20 @@ class _BlockFn(torch.autograd.Function):
         batch, seq, dim = x.shape
         x2 = _as_rows(x).contiguous()
         n1, mu1, rs1 = ln_fwd(x2, g1, b1, eps)
-        qkv, c, lse, head_dim = _attention_forward(n1, wq, wk, wv, num_heads, batch, seq)
+        qkv, c, lse, c_lo, head_dim = _attention_forward(n1, wq, wk, wv, num_heads, batch, seq)
         x1 = linear_fwd(c, [wo], residual=x2)
         n2, mu2, rs2 = ln_fwd(x1, g2, b2, eps)
         gd = _rows(x2.shape[0], w1.shape[0], x2)  # gelu'(fc1 output), kept for the backward
         h = linear_fwd(n2, [w1], gelu_deriv=gd)
         out = linear_fwd(h, [w2], residual=x1)
-        ctx.save_for_backward(x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, gd, h)
+        ctx.save_for_backward(x2, n1, mu1, rs1, qkv, c, lse, c_lo, x1, n2, mu2, rs2, gd, h)
         ctx.params = (g1, b1, wq, wk, wv, wo, g2, b2, w1, w2)
         ctx.meta = (batch, seq, num_heads, head_dim)
         return out.view(batch, seq, dim)
 
     @staticmethod
     def backward(ctx, dout):
-        x2, n1, mu1, rs1, qkv, c, lse, x1, n2, mu2, rs2, gd, h = ctx.saved_tensors
+        x2, n1, mu1, rs1, qkv, c, lse, c_lo, x1, n2, mu2, rs2, gd, h = ctx.saved_tensors
         g1, b1, wq, wk, wv, wo, g2, b2, w1, w2 = ctx.params
         batch, seq, num_heads, head_dim = ctx.meta
         d2 = _as_rows(dout).contiguous()
@@ -530,7 +539,7 @@ class _BlockFn(torch.autograd.Function):
         # attention branch
         dctx = linear_dgrad(dx1, [wo])
         linear_wgrad(dx1, c, [wo])
-        dn1 = _attention_backward(dctx, n1, qkv, c, lse, wq, wk, wv, num_heads, head_dim, batch, seq)
+        dn1 = _attention_backward(dctx, n1, qkv, c, lse, c_lo, wq, wk, wv, num_heads, head_dim, batch, seq)
         dx = ln_bwd(dn1, x2, mu1, rs1, g1, b1, dres=dx1)
         return (dx.view(batch, seq, -1),) + (None,) * 12
 
@@ -563,9 +572,12 @@ class _NextTokenLossFn(torch.autograd.Function):
             dl = torch.empty((rows, ld_d), dtype=logits.dtype, device=dev)
         nbytes = H.query("rh_xent_workspace_bytes", batch, seq)
         ws = H.workspace(nbytes, dev)
-        H.call("rh_xent_fwd", H.dtype_code(logits), batch, seq, vocab, logits.data_ptr(), ld, tokens.data_ptr(),
-               lse.data_ptr(), loss.data_ptr(), H.ptr(dl), 0 if dl is None else dl.shape[1], H.ptr(ws), nbytes,
-               H.stream_of(logits))
+        es = logits.element_size()
+        moved = rows * vocab * es * (1 if dl is None else 2) + 12 * rows  # logits (+ dlogits), tokens, lse
+        with profiling.launch("xent_fwd" if dl is None else "xent_fwd (+ dlogits)", 0.0, moved):
+            H.call("rh_xent_fwd", H.dtype_code(logits), batch, seq, vocab, logits.data_ptr(), ld, tokens.data_ptr(),
+                   lse.data_ptr(), loss.data_ptr(), H.ptr(dl), 0 if dl is None else dl.shape[1], H.ptr(ws), nbytes,
+                   H.stream_of(logits))
         ctx.save_for_backward(logits, tokens, lse)
         ctx.dl = dl
         ctx.shape = (batch, seq, vocab)

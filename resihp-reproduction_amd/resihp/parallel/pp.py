@@ -24,6 +24,14 @@ def run_1f1b(stage, *, stage_index: int, num_stages: int, inputs=None, tokens=No
     sent back by the next stage (ignored on a last stage, which backpropagates its loss).
     Returns ``(order, total_loss)``; ``total_loss`` is ``None`` unless the stage is last.
     """
+    if stage.is_last and stage.tp_size > 1:
+        # The reference scores the all-gathered full-vocabulary logits (pp.py:375-384 after
+        # tp.py:92-110); one rank's stage only holds its [batch, seq, vocab/tp] slice, and a
+        # cross-entropy over that slice has the wrong normaliser (and no target for most rows).
+        raise NotImplementedError(
+            "run_1f1b on a last stage with tp_size > 1 needs the all-gathered logits of every TP rank; "
+            "this build computes one rank per GPU without collectives"
+        )
     count = len(tokens) if stage.is_first else len(inputs)
     if not stage.is_last and (grads is None or len(grads) != count):
         raise ValueError("a non-last stage needs one returned gradient per micro-batch")

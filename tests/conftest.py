@@ -32,8 +32,10 @@ def rel_inf(a, b) -> float:
     """max|a - b| / max|b| (the reference's own band form, tests/test_reference.py:154-156)."""
     import torch
 
-    a = a.detach().double().cpu()
-    b = b.detach().double().cpu()
+    # computed in fp64 on b's device (a GPU for the full-size workloads, whose logits alone
+    # are 4e8 elements)
+    b = b.detach().double()
+    a = a.detach().to(b.device).double()
     scale = b.abs().max().item()
     diff = (a - b).abs().max().item()
     return diff / scale if scale > 0 else diff

@@ -247,7 +247,7 @@ def _attn_ref(q, k, v, heads):
 def test_attention_forward_backward(cuda, dtype, head_dim, seq, heads, batch):
     W = heads * head_dim
     qkv = _rand(batch * seq, 3 * W, dtype=dtype, seed=20)
-    ctx, lse = ops.attn_fwd(qkv, batch, seq, heads, head_dim)
+    ctx, lse, ctx_lo = ops.attn_fwd(qkv, batch, seq, heads, head_dim)
     q, k, v = (qkv[:, i * W:(i + 1) * W].reshape(batch, seq, W).float().requires_grad_(True) for i in range(3))
     ref = _attn_ref(q, k, v, heads)
     tol = 2e-2 if dtype == torch.bfloat16 else F32_TOL
@@ -259,11 +259,14 @@ def test_attention_forward_backward(cuda, dtype, head_dim, seq, heads, batch):
     s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool, device=cuda), 1), float("-inf"))
     assert rel_inf(lse, torch.logsumexp(s, -1)) <= (1e-5 if dtype == torch.float32 else 5e-3)
     dout = _rand(batch * seq, W, dtype=dtype, seed=21)
-    dqkv = ops.attn_bwd(dout, qkv, ctx, lse, batch, seq, heads, head_dim)
+    dqkv = ops.attn_bwd(dout, qkv, ctx, lse, batch, seq, heads, head_dim, ctx_lo)
     ref.backward(dout.float().view(batch, seq, W))
+    errs = {}
     for i, t in enumerate((q, k, v)):
-        got = dqkv[:, i * W:(i + 1) * W].reshape(batch, seq, W)
-        assert rel_inf(got, t.grad) <= (3e-2 if dtype == torch.bfloat16 else 1e-4), ("qkv"[i], rel_inf(got, t.grad))
+        errs["d" + "qkv"[i]] = rel_inf(dqkv[:, i * W:(i + 1) * W].reshape(batch, seq, W), t.grad)
+    print({k: f"{e:.2e}" for k, e in errs.items()})
+    for name, err in errs.items():
+        assert err <= (2e-2 if dtype == torch.bfloat16 else 1e-4), (name, err)
 
 
 @pytest.mark.parametrize("dtype,rows,dim", [(torch.float32, 64, 64), (torch.float32, 37, 100),
@@ -455,3 +458,82 @@ def test_gemm_unaligned_views(cuda, gemm_tile):
     assert rel_inf(U, pre) <= BF16_TOL
     assert rel_inf(D, F.gelu(pre)) <= BF16_TOL
     assert torch.all(Dbuf[:, 0] == 0) and torch.all(Ubuf[:, :5] == 0)  # nothing written outside the views
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_adamw_multi_tensor_matches_torch(cuda, dtype):
+    """adamw(params).step() over every parameter of the tiny LM (2 layers, d 64, vocab 256, seq 32;
+    25 tensors) plus 110 extra tensors of ragged sizes (one empty), so the update spans several
+    64-tensor launches: 3 steps against torch.optim.AdamW with the reference's constants, fp32
+    within 1e-6 (params and both moments); bf16 against the same fp32 update, within the three
+    roundings of the stored bf16 values (each at most half an ulp, 2^-8 of the value at the bottom
+    of a binade); device step counts equal 3."""
+    from resihp.config import TrainConfig
+    from resihp.model import ReferenceTransformer
+    from resihp.reference import adamw
+
+    cfg = TrainConfig(model_dim=64, num_layers=2, num_heads=4, batch_size=4, micro_batch_size=4, seed=1234, tp=1,
+                      pp=1, dp=1, iterations=1)
+    torch.manual_seed(1234)
+    model = ReferenceTransformer(cfg, vocab_size=256, sequence_length=32)
+    params = [torch.nn.Parameter(p.detach().clone()) for p in model.parameters()]
+    g = torch.Generator().manual_seed(90)
+    params += [torch.nn.Parameter(torch.randn(n, generator=g) * 0.1) for n in list(range(0, 100)) + [1000 + 37 * i for i in range(10)]]
+    ours = [torch.nn.Parameter(p.detach().to(cuda, dtype)) for p in params]
+    ref = [torch.nn.Parameter(p.detach().to(cuda, dtype).float()) for p in params]
+    opt = adamw(ours)
+    ref_opt = torch_ref.adamw(ref)
+    for step in range(3):
+        for a, b in zip(ours, ref):
+            gr = torch.randn(a.shape, generator=g).to(cuda)
+            a.grad = gr.to(dtype)
+            b.grad = gr.to(dtype).float()
+        opt.step()
+        ref_opt.step()
+    tol = 1e-6 if dtype == torch.float32 else 3 * 2.0 ** -8
+    for i, (a, b) in enumerate(zip(ours, ref)):
+        if a.numel() == 0:
+            continue
+        sa, sb = opt.state[a], ref_opt.state[b]
+        assert float(sa["step"]) == 3.0
+        assert rel_inf(a, b) <= tol, (i, "param", rel_inf(a, b))
+        assert rel_inf(sa["exp_avg"], sb["exp_avg"]) <= tol, (i, "exp_avg")
+        assert rel_inf(sa["exp_avg_sq"], sb["exp_avg_sq"]) <= 2 * tol, (i, "exp_avg_sq")
+
+
+def test_adamw_multi_rejects_shared_step_counters(cuda):
+    p = torch.zeros(8, device=cuda)
+    step = torch.zeros((), device=cuda)
+    e = H.rh_adamw_tensor(p.data_ptr(), p.data_ptr(), p.data_ptr(), p.data_ptr(), step.data_ptr(), 8)
+    arr = (H.rh_adamw_tensor * 2)(e, e)
+    with pytest.raises(ValueError, match="share a step counter"):
+        H.call("rh_adamw_multi", H.RH_DTYPE_F32, 2, arr, 1e-3, 0.9, 0.999, 1e-8, 0.01, None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,seq,vocab,repeat", [
+    (32, 1024, 50257, 0.7),   # 32768 tokens, 70 % of them one id: a 23k-row segment
+    (16, 1024, 50257, 0.0),   # GPT-2-small vocabulary, uniform ids
+    (3, 4097, 40, 0.5),       # ragged token count, few ids: every chunk boundary inside a segment
+    (1, 20000, 1, 0.0),       # a single id for every token
+])
+def test_embedding_backward_any_token_count(cuda, dtype, batch, seq, vocab, repeat):
+    """Token-embedding gradient beyond one workgroup's sort: 32768 tokens with one id repeated
+    ~23k times, ragged counts, a one-row vocabulary -- against an fp64 index_add, and bit-identical
+    on a second run."""
+    dim = 64 if dtype == torch.bfloat16 else 48
+    g = torch.Generator().manual_seed(55)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g)
+    tokens[torch.rand(batch, seq, generator=g) < repeat] = vocab // 2
+    tokens = tokens.to(cuda)
+    W = torch.nn.Parameter(torch.zeros(vocab, dim, device=cuda, dtype=dtype))
+    dout = _rand(batch, seq, dim, dtype=dtype, seed=56)
+    out = ops.embedding(tokens, W)
+    out.backward(dout)
+    first = W.grad.clone()
+    want = torch.zeros(vocab, dim, device=cuda, dtype=torch.float64)
+    want.index_add_(0, tokens.reshape(-1), dout.double().reshape(-1, dim))
+    assert rel_inf(first, want) <= (1e-6 if dtype == torch.float32 else 4e-3)
+    W.grad = None
+    ops.embedding(tokens, W).backward(dout)
+    assert torch.equal(W.grad, first)

@@ -46,7 +46,7 @@ def test_library_version_and_argument_errors():
     with pytest.raises(ValueError, match="unknown layout"):
         _hip.call("rh_gemm", ctypes.byref(desc), None, 0, None)
     with pytest.raises(ValueError, match="head_dim"):
-        _hip.call("rh_attn_fwd", 1, 1, 8, 1, 256, None, None, None, 256, None, 256, None, 1.0, 1, None)
+        _hip.call("rh_attn_fwd", 1, 1, 8, 1, 256, None, None, None, 256, None, None, 256, None, 1.0, 1, None)
     with pytest.raises(ValueError, match="shard_dim"):
         ext = (ctypes.c_int64 * 1)(4)
         _hip.call("rh_reshard_pack", (ctypes.c_void_p * 1)(None), ext, 1, 4, 4, 2, 2, None, None)
@@ -205,3 +205,23 @@ def test_profiling_short_name_strips_namespaces_and_parameters():
     # template arguments that name namespaced types are kept whole
     torch_k = "void at::native::vectorized_elementwise_kernel<8, at::native::FillFunctor<float> >(int, float)"
     assert _short_name(torch_k) == "vectorized_elementwise_kernel<8, at::native::FillFunctor<float> >"
+
+
+def test_1f1b_refuses_a_vocab_parallel_last_stage():
+    """A last stage with tp_size > 1 holds only its vocabulary slice of the logits; the reference
+    scores the all-gathered logits (parallel/pp.py:375-384), so run_1f1b refuses instead of
+    computing a cross-entropy over the slice."""
+    from resihp.parallel.pp import run_1f1b
+
+    torch.manual_seed(3)
+    ref = ReferenceTransformer(TrainConfig(model_dim=16, num_layers=1, num_heads=4, batch_size=4,
+                                           micro_batch_size=2, seed=3, tp=1, pp=1, dp=1, iterations=1),
+                               vocab_size=32, sequence_length=8)
+    layout = reshard.shard_dims([0])
+    full = ref.logical_state_dict()
+    local = {n: torch.chunk(full[n], 2, d)[0].contiguous() if d is not None else full[n].detach()
+             for n, d in layout.items()}
+    stage = TensorParallelStage(ref.config, vocab_size=32, sequence_length=8, layer_ids=[0], is_first=False,
+                                is_last=True, local_state=local, tp_rank=0, tp_size=2)
+    with pytest.raises(NotImplementedError, match="all-gathered"):
+        run_1f1b(stage, stage_index=1, num_stages=2, inputs=[torch.zeros(2, 8, 16)], tokens=[torch.zeros(2, 8)])
