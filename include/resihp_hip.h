@@ -158,6 +158,22 @@ int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t he
                 const float* lse, void* dq, void* dk, void* dv, int64_t ld_dqkv, float scale,
                 int causal, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* rh_attn_bwd_noalloc: rh_attn_bwd with no workspace argument and no allocation of any
+ * kind -- for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The backward's scratch (delta, one fp32 per query row) lives in a static device array
+ * of RH_ATTN_NOALLOC_MAX_ROWS floats (8 MiB, held by every GPU the library runs on until
+ * the process ends); batch*seq*heads above that limit is rejected (RH_ERR_INVALID).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must not be issued; calls in one stream's order are
+ * safe.  Results equal rh_attn_bwd's bit for bit. */
+#define RH_ATTN_NOALLOC_MAX_ROWS 2097152
+int rh_attn_bwd_noalloc(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                        const void* q, const void* k, const void* v, int64_t ld_qkv,
+                        const void* o, const void* o_lo, int64_t ld_o, const void* dout, int64_t ld_do,
+                        const float* lse, void* dq, void* dk, void* dv, int64_t ld_dqkv, float scale,
+                        int causal, void* stream);
+
 /* ---- LayerNorm ----------------------------------------------------------------
  * Replaces nn.LayerNorm / F.layer_norm over the last dim, eps default 1e-5,
  * biased variance (resihp/model.py:89,91,95-96,115,132;

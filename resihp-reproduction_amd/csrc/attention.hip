@@ -32,11 +32,13 @@
 // Everything else (fp32, other head sizes): one thread per query (forward, dq)
 // or per key (dk/dv) with K/V or Q/dO tiles staged in LDS; fp32 FMA.
 #include <initializer_list>
+#include <mutex>
 
 #include "common.hpp"
 
 namespace {
 
+constexpr int kMaxDevices = 64;
 constexpr float kLog2e = 1.4426950408889634074f;
 constexpr float kLn2 = 0.69314718055994530942f;
 
@@ -1013,25 +1015,29 @@ extern "C" int rh_attn_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t h
   return RH_OK;
 }
 
-extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, const void* q,
-                           const void* k, const void* v, int64_t ld_qkv, const void* o, const void* o_lo, int64_t ld_o,
-                           const void* dout, int64_t ld_do, const float* lse, void* dq, void* dk, void* dv,
-                           int64_t ld_dqkv, float scale, int causal, void* workspace, int64_t workspace_bytes,
-                           void* stream) {
+static int attn_bwd_check(const char* who, int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                          const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o, int64_t ld_o,
+                          const void* dout, int64_t ld_do, const float* lse, void* dq, void* dk, void* dv,
+                          int64_t ld_dqkv, float scale) {
   int rc = check_common(dtype, batch, seq, heads, head_dim);
   if (rc) return rc;
   if (batch == 0 || seq == 0 || heads == 0) return RH_OK;
-  RH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "rh_attn_bwd: null pointer");
-  RH_REQUIRE(scale > 0.f, "rh_attn_bwd: scale must be positive (got %g)", (double)scale);
+  RH_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "%s: null pointer", who);
+  RH_REQUIRE(scale > 0.f, "%s: scale must be positive (got %g)", who, (double)scale);
   const int64_t width = heads * head_dim;
   RH_REQUIRE(ld_qkv >= width && ld_o >= width && ld_do >= width && ld_dqkv >= width,
-             "rh_attn_bwd: leading dimension too small");
-  RH_REQUIRE(workspace && workspace_bytes >= batch * seq * heads * (int64_t)sizeof(float),
-             "rh_attn_bwd: workspace of %lld bytes is too small", (long long)workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  float* delta = static_cast<float*>(workspace);
-  const int64_t rows = batch * seq * heads;
-  const unsigned dblocks = (unsigned)((rows + 255) / 256);
+             "%s: leading dimension too small", who);
+  return RH_OK;
+}
+
+// The backward after the argument checks.  `delta` holds batch*seq*heads floats; every row is
+// written (by the dQ kernel or attn_delta) before the dK/dV pass reads it, so its previous
+// contents do not matter.
+static int attn_bwd_launch(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, const void* q,
+                           const void* k, const void* v, int64_t ld_qkv, const void* o, const void* o_lo,
+                           int64_t ld_o, const void* dout, int64_t ld_do, const float* lse, void* dq, void* dk,
+                           void* dv, int64_t ld_dqkv, float scale, int causal, float* delta, hipStream_t st) {
+  const int64_t rows = batch * seq * heads;  const unsigned dblocks = (unsigned)((rows + 255) / 256);
   if (dtype == RH_DTYPE_BF16) {
     AttnArgs<bf16_t> a = make_args<bf16_t>(batch, seq, heads, head_dim, scale, causal);
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.ld_qkv = ld_qkv;
@@ -1063,4 +1069,64 @@ extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads,
     dispatch_generic(a, st, false);
   }
   return rh_check_launch("rh_attn_bwd");
+}
+
+extern "C" int rh_attn_bwd(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, const void* q,
+                           const void* k, const void* v, int64_t ld_qkv, const void* o, const void* o_lo, int64_t ld_o,
+                           const void* dout, int64_t ld_do, const float* lse, void* dq, void* dk, void* dv,
+                           int64_t ld_dqkv, float scale, int causal, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  int rc = attn_bwd_check("rh_attn_bwd", dtype, batch, seq, heads, head_dim, q, k, v, ld_qkv, o, ld_o, dout, ld_do,
+                          lse, dq, dk, dv, ld_dqkv, scale);
+  if (rc || batch == 0 || seq == 0 || heads == 0) return rc;
+  RH_REQUIRE(workspace && workspace_bytes >= batch * seq * heads * (int64_t)sizeof(float),
+             "rh_attn_bwd: workspace of %lld bytes is too small", (long long)workspace_bytes);
+  return attn_bwd_launch(dtype, batch, seq, heads, head_dim, q, k, v, ld_qkv, o, o_lo, ld_o, dout, ld_do, lse, dq, dk,
+                         dv, ld_dqkv, scale, causal, static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// rh_attn_bwd_noalloc: the same backward with its delta rows in a static device array.
+// In host code `scratch` is only a stand-in for the array: its address on the current GPU
+// comes from hipGetSymbolAddress, once per device, and only that address reaches a kernel.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[RH_ATTN_NOALLOC_MAX_ROWS];
+
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices] = {};
+
+static int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return rh_set_error(RH_ERR_HIP, "rh_attn_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  RH_REQUIRE(dev >= 0 && dev < kMaxDevices, "rh_attn_bwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return rh_set_error(RH_ERR_HIP, "rh_attn_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                          hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return RH_OK;
+}
+
+extern "C" int rh_attn_bwd_noalloc(int dtype, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                                   const void* q, const void* k, const void* v, int64_t ld_qkv, const void* o,
+                                   const void* o_lo, int64_t ld_o, const void* dout, int64_t ld_do, const float* lse,
+                                   void* dq, void* dk, void* dv, int64_t ld_dqkv, float scale, int causal,
+                                   void* stream) {
+  int rc = attn_bwd_check("rh_attn_bwd_noalloc", dtype, batch, seq, heads, head_dim, q, k, v, ld_qkv, o, ld_o, dout,
+                          ld_do, lse, dq, dk, dv, ld_dqkv, scale);
+  if (rc || batch == 0 || seq == 0 || heads == 0) return rc;
+  RH_REQUIRE(batch * seq * heads <= RH_ATTN_NOALLOC_MAX_ROWS,
+             "rh_attn_bwd_noalloc: batch*seq*heads = %lld query rows exceeds the static scratch of %d rows",
+             (long long)(batch * seq * heads), RH_ATTN_NOALLOC_MAX_ROWS);
+  float* delta = nullptr;
+  rc = scratch_on_current_device(&delta);
+  if (rc) return rc;
+  return attn_bwd_launch(dtype, batch, seq, heads, head_dim, q, k, v, ld_qkv, o, o_lo, ld_o, dout, ld_do, lse, dq, dk,
+                         dv, ld_dqkv, scale, causal, delta, static_cast<hipStream_t>(stream));
 }

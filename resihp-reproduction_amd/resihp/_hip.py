@@ -108,6 +108,8 @@ _SIGNATURES = {
     "rh_attn_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],
     "rh_attn_bwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                     c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_float, c_int, c_ptr, c_i64, c_ptr],
+    "rh_attn_bwd_noalloc": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr,
+                            c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_float, c_int, c_ptr],
     "rh_layernorm_fwd": [c_int, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_float, c_ptr, c_ptr, c_ptr, c_ptr],
     "rh_layernorm_bwd_workspace_bytes": [c_i64, c_i64, ctypes.POINTER(c_i64)],
     "rh_layernorm_bwd": [c_int, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_int,
