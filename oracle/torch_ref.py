@@ -268,3 +268,25 @@ def issue_order(num_micro, stage_index, num_stages):
         else:
             out.append(f"B{held.pop(0)}")
     return out
+
+
+def scatter_routing(up, down):
+    """parallel/pp.py:57-80: chunk k of N = max(U, D) travels up[k*U//N] -> down[k*D//N]."""
+    n = max(len(up), len(down))
+    return [(up[k * len(up) // n], down[k * len(down) // n]) for k in range(n)]
+
+
+def boundary_slab(tensor, up, down, rank, backward=False):
+    """The slab one rank of a pipeline hop collects (parallel/pp.py:262-281): the chunks of the
+    flattened boundary tensor routed to it, in chunk order (forward: downstream receivers;
+    backward: the same pairs reversed, upstream receivers)."""
+    flat = tensor.reshape(-1)
+    routing = scatter_routing(up, down)
+    width = flat.numel() // len(routing)
+    end = 0 if backward else 1
+    return torch.cat([flat[k * width:(k + 1) * width] for k, pair in enumerate(routing) if pair[end] == rank])
+
+
+def boundary_reconstruct(slabs, shape):
+    """parallel/pp.py:283-295: the stage's slabs in TP-rank order, concatenated."""
+    return torch.cat(list(slabs)).view(shape)

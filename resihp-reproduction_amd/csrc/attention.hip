@@ -682,6 +682,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     const int wq0 = it.blk * 64 + 32 * sub, wq1 = wq0 + 31, q_row = wq0 + l32;
     const bool qok = q_row < S;
 
+    // the first K/V stage goes out before the row loads below, so its latency overlaps theirs
+    const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
+    const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
+    const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
+    const int nst = (kv_end + kStageRows - 1) / kStageRows;
+    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
+    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
+
     bf16x8_t qreg[KS], doreg[KS];
     load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, qok, g);
     load_head_row<KS>(doreg, a.dout + (tok0 + q_row) * a.ld_do + (int64_t)h * D, qok, g);
@@ -707,13 +715,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     floatx16_t dqt[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) dqt[d] = zero16();
-
-    const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
-    const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
-    const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
-    const int nst = (kv_end + kStageRows - 1) / kStageRows;
-    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
-    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
     wait_vm();
     __syncthreads();
     for (int t = 0; t < nst; ++t) {

@@ -344,3 +344,27 @@ def test_pp_stage_1f1b_matches_fp32_oracle(cuda):
     print(f"1F1B stage bf16 vs fp32 oracle: worst {worst} {errs[worst]:.2e}")
     for name, err in errs.items():
         assert err <= 2e-2, (name, err)
+
+
+@pytest.mark.parametrize("up,down", [((0,), (1,)), ((0, 1), (2, 3)), ((0, 1), (2,)), ((0,), (1, 2)),
+                                     ((0, 1, 2, 3), (4, 5)), ((0, 1), (2, 3, 4, 5, 6, 7, 8, 9))])
+def test_pp_boundary_slabs_are_bit_exact(cuda, up, down):
+    """A PP hop's boundary activation [2, 2048, 2048] bf16 (one 1F1B micro-batch of the d 2048 stage)
+    and its gradient, scattered over the hop's rank pairs into bf16 slabs and rebuilt by the receiving
+    stage: every slab equals the oracle's chunks (parallel/pp.py:242-295 restated), and the rebuilt
+    tensors equal the originals bit for bit."""
+    from resihp.parallel import boundary
+
+    g = torch.Generator().manual_seed(77)
+    act = torch.randn(2, 2048, 2048, generator=g).to(torch.bfloat16)
+    grad = (torch.randn(2, 2048, 2048, generator=g) * 1e-2).to(torch.bfloat16)
+    for t, backward in ((act, False), (grad, True)):
+        slabs = boundary.exchange(t.to(cuda), up, down, backward=backward)
+        receivers = up if backward else down
+        assert sorted(slabs) == sorted(receivers)
+        for r in receivers:
+            assert slabs[r].dtype == torch.bfloat16
+            assert torch.equal(slabs[r].cpu(), torch_ref.boundary_slab(t, up, down, r, backward)), (r, backward)
+        rebuilt = boundary.reconstruct([slabs[r] for r in receivers], t.shape)
+        assert torch.equal(rebuilt.cpu(), t)
+        assert torch.equal(torch_ref.boundary_reconstruct([slabs[r].cpu() for r in receivers], t.shape), t)

@@ -225,3 +225,40 @@ def test_1f1b_refuses_a_vocab_parallel_last_stage():
                                 is_last=True, local_state=local, tp_rank=0, tp_size=2)
     with pytest.raises(NotImplementedError, match="all-gathered"):
         run_1f1b(stage, stage_index=1, num_stages=2, inputs=[torch.zeros(2, 8, 16)], tokens=[torch.zeros(2, 8)])
+
+
+# the reference's own routing cases (tests/test_parallel_pp.py:95-101) and properties (:106-141)
+_ROUTING_CASES = [((0,), (1,)), ((0, 1), (2, 3)), ((0, 1), (2,)), ((0,), (1, 2)), ((0, 1, 2, 3), (4, 5))]
+
+
+@pytest.mark.parametrize("up,down", _ROUTING_CASES)
+def test_boundary_routing_spreads_one_copy_over_n_links(up, down):
+    from resihp.parallel.boundary import scatter_routing
+
+    routing = scatter_routing(up, down)
+    chunks = max(len(up), len(down))
+    assert len(routing) == chunks and len(set(routing)) == chunks
+    for members, end in ((up, 0), (down, 1)):
+        runs = [[k for k, pair in enumerate(routing) if pair[end] == m] for m in members]
+        assert all(runs)
+        for run in runs:
+            assert run == list(range(run[0], run[0] + len(run))) and len(run) == chunks // len(members)
+        assert [k for run in runs for k in run] == list(range(chunks))
+
+
+def test_boundary_chunks_and_send_views():
+    from resihp.parallel.boundary import my_chunks, scatter_routing, scatter_send_chunks
+
+    assert scatter_routing((0, 1, 2, 3), (4, 5)) == ((0, 4), (1, 4), (2, 5), (3, 5))
+    assert my_chunks(4, (0, 1, 2, 3), (4, 5)) == ((0, 0), (1, 1))
+    assert my_chunks(2, (0, 1, 2, 3), (4, 5)) == ((2, 5),)
+    assert my_chunks(0, (0,), (1, 2)) == ((0, 1), (1, 2))
+    with pytest.raises(ValueError):
+        my_chunks(9, (0,), (1,))
+    t = torch.arange(24.0).reshape(2, 3, 4)
+    sends = scatter_send_chunks(t, 0, (0,), (1, 2))
+    assert [p for p, _ in sends] == [1, 2]
+    assert torch.equal(torch.cat([c for _, c in sends]), t.reshape(-1))
+    assert sends[1][1].data_ptr() == t.reshape(-1)[12:].data_ptr()  # a view, not a copy
+    with pytest.raises(ValueError, match="equal chunks"):
+        scatter_send_chunks(torch.zeros(5), 0, (0,), (1, 2))
