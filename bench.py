@@ -246,6 +246,20 @@ class GPT2Small(Workload):
                           f"torch-CPU restatement; median of 3 after 1 warm-up"}
 
 
+class GPT2SmallFused(GPT2Small):
+    """GPT-2-small with the LM head fused into the cross-entropy (no [8, 1024, 50257] logits or
+    logit-gradient tensors; the backward recomputes the logits in vocabulary chunks)."""
+
+    def __init__(self):
+        super().__init__(name="gpt2_small_lm_fused_head")
+        self.flops += 2.0 * self.tokens * self.d * self.vocab  # the backward's logit recompute
+        self.config["lm_head"] = "fused with the cross-entropy (logits recomputed in the backward)"
+
+    def step(self):
+        self.loss = self.model.next_token_loss(self.tok)
+        self.loss.backward()
+
+
 class PPStage(ShardBlock):
     """One 1F1B pipeline stage: 6 of 24 layers (d 2048, 16 heads, FFN 8192), 8 micro-batches of 2x2048."""
 
@@ -385,6 +399,7 @@ def xent_leg(dev, reps=5):
 WORKLOADS = {
     "tp4_shard_gpt1.3b_block": lambda: ShardBlock("tp4_shard_gpt1.3b_block"),
     "gpt2_small_lm": GPT2Small,
+    "gpt2_small_lm_fused_head": GPT2SmallFused,
     "pp_stage_1f1b": PPStage,
     "tp2_shard_after_reshard": lambda: ReshardShard("tp2_shard_after_reshard", d=2048, heads=16, tp=2, rank=1,
                                                     seq=2048, batch=2),

@@ -130,6 +130,24 @@ int rh_gemm_stage(const rh_gemm_desc* desc, void* workspace, int64_t workspace_b
  * attributing profiler records.  No counterpart in the reference (profiling support). */
 int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t len);
 
+/* Grouped GEMMs: up to 4 problems of one layout in ONE launch -- the weight gradients of a
+ * decoder block (fc2, fc1, out_proj and the fused q/k/v: dW = dY^T X with the token count
+ * as K, resihp/parallel/tp.py:235-248 and their autograd backward), so the block's wgrads
+ * fill the chip together instead of each needing a split-K pass of its own.  Every
+ * descriptor is an ordinary rh_gemm descriptor (beta/C accumulation into .grad and
+ * segmented D included); each problem's result equals rh_gemm's up to the order of the
+ * split-K partial sums.  The group runs in one launch (plus one reduce per problem when
+ * the planner splits K) when all are bf16, of one layout, RH_EPI_NONE, K a multiple of 64
+ * and the operands 16-byte aligned; otherwise, or with a smaller workspace than queried,
+ * the problems run as consecutive rh_gemm calls.  rh_gemm_grouped_plan reports the split
+ * count the single launch would use (0: consecutive calls).  No counterpart in the
+ * reference beyond the GEMMs themselves. */
+#define RH_GEMM_MAX_GROUP 4
+int rh_gemm_grouped_workspace_bytes(const rh_gemm_desc* descs, int n, int64_t* bytes);
+int rh_gemm_grouped(const rh_gemm_desc* descs, int n, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+int rh_gemm_grouped_plan(const rh_gemm_desc* descs, int n, int* splits);
+
 /* ---- causal self-attention core ---------------------------------------------
  * Replaces  scores = q @ k^T / sqrt(Dh); masked_fill(triu(ones,1), -inf);
  * softmax(-1); @ v   (resihp/model.py:62-70, resihp/parallel/tp.py:231-242)
@@ -263,6 +281,30 @@ int rh_xent_fwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void
 int rh_xent_bwd(int dtype, int64_t batch, int64_t seq, int64_t vocab, const void* logits,
                 int64_t ld, const int64_t* tokens, const float* row_lse, const float* grad_loss,
                 void* dlogits, int64_t ld_d, void* stream);
+
+/* ---- LM head fused with the next-token cross-entropy -------------------------------
+ * Replaces  logits = lm_head(final_norm(x))  (resihp/model.py:116,133; the vocab-parallel
+ * head and its gather, resihp/parallel/tp.py:92-110,269-273) followed by next_token_loss
+ * (resihp/reference.py:41-50), bf16 only, without materialising the [batch*seq, vocab]
+ * logits or their gradient.  x [batch*seq, dim] (the final LayerNorm's output) and
+ * W [vocab, dim] row-major, dim a multiple of 64; tokens int64 [batch, seq].
+ * rh_lmhead_xent_fwd: loss [1] = mean over the batch*(seq-1) scored rows of
+ *   lse - logit[target]; row_lse [batch*seq] (0 on each sequence's last position).  The
+ *   GEMM's epilogue keeps only per-row (max, sum-exp) partials of each 64-column block.
+ * rh_lmhead_xent_bwd: dx [batch*seq, dim] = dS . W and dW (+)= dS^T . x (accumulate != 0
+ *   adds to dW, e.g. a parameter's .grad) for dS = (softmax - onehot) * *grad_loss / N,
+ *   recomputing the logits vocabulary chunk by chunk (8192 ids): each chunk's dS lives in
+ *   a reused workspace buffer, dx is summed over the chunks in fp32 and rounded once.
+ * Workspace sizes come from rh_lmhead_xent_workspace_bytes (256-byte aligned). */
+int rh_lmhead_xent_workspace_bytes(int64_t batch, int64_t seq, int64_t vocab, int64_t dim,
+                                   int64_t* fwd_bytes, int64_t* bwd_bytes);
+int rh_lmhead_xent_fwd(int64_t batch, int64_t seq, int64_t vocab, int64_t dim, const void* x,
+                       const void* w, const int64_t* tokens, float* row_lse, float* loss,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+int rh_lmhead_xent_bwd(int64_t batch, int64_t seq, int64_t vocab, int64_t dim, const void* x,
+                       const void* w, const int64_t* tokens, const float* row_lse,
+                       const float* grad_loss, void* dx, void* dw, int accumulate,
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- embeddings ------------------------------------------------------------------
  * Forward: out[b,s,:] = tok[ids[b,s] - vocab_start, :] (zero row when the id is

@@ -36,6 +36,9 @@ extern template int launch_layout<float, RH_GEMM_TN, RH_EPI_GELU>(const rh_gemm_
 extern template int launch_layout<float, RH_GEMM_TN, RH_EPI_GELU_GRAD>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
 extern template int launch_layout<float, RH_GEMM_TN, RH_EPI_GELU_DERIV>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
 extern template int launch_layout<float, RH_GEMM_TN, RH_EPI_MUL_AUX>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
+extern template int launch_grouped<RH_GEMM_NT>(const rh_gemm_desc*, int, const GroupPlan&, void*, hipStream_t);
+extern template int launch_grouped<RH_GEMM_NN>(const rh_gemm_desc*, int, const GroupPlan&, void*, hipStream_t);
+extern template int launch_grouped<RH_GEMM_TN>(const rh_gemm_desc*, int, const GroupPlan&, void*, hipStream_t);
 
 template <typename T, int EPI>
 int launch_epi(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st, int stage) {
@@ -143,4 +146,54 @@ extern "C" int rh_gemm_stage(const rh_gemm_desc* desc, void* workspace, int64_t 
   }
   return bf16 ? launch_dtype<bf16_t>(desc, pl, workspace, st, stage)
               : launch_dtype<float>(desc, pl, workspace, st, stage);
+}
+
+extern "C" int rh_gemm_grouped_workspace_bytes(const rh_gemm_desc* descs, int n, int64_t* bytes) {
+  RH_REQUIRE(bytes != nullptr, "rh_gemm_grouped_workspace_bytes: null output");
+  RH_REQUIRE(n >= 0 && (n == 0 || descs), "rh_gemm_grouped_workspace_bytes: bad descriptor list");
+  int64_t most = 0;
+  for (int i = 0; i < n; ++i) {
+    int64_t b = 0;
+    int rc = rh_gemm_workspace_bytes(&descs[i], &b);
+    if (rc) return rc;
+    most = std::max(most, b);
+  }
+  const GroupPlan g = plan_grouped(descs, n);
+  *bytes = g.ok ? g.ws_off[n] : most;
+  return RH_OK;
+}
+
+extern "C" int rh_gemm_grouped(const rh_gemm_desc* descs, int n, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  RH_REQUIRE(n >= 0 && (n == 0 || descs), "rh_gemm_grouped: bad descriptor list");
+  for (int i = 0; i < n; ++i) {
+    int rc = validate(&descs[i]);
+    if (rc) return rc;
+  }
+  const GroupPlan g = plan_grouped(descs, n);
+  const bool room = g.ok && (g.ws_off[n] == 0 || (workspace && workspace_bytes >= g.ws_off[n] && rh_aligned(workspace, 16)));
+  if (!room) {  // one call per descriptor (each plans its own split within the same workspace)
+    for (int i = 0; i < n; ++i) {
+      int rc = rh_gemm(&descs[i], workspace, workspace_bytes, stream);
+      if (rc) return rc;
+    }
+    return RH_OK;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (descs[0].layout) {
+    case RH_GEMM_NT: return launch_grouped<RH_GEMM_NT>(descs, n, g, workspace, st);
+    case RH_GEMM_NN: return launch_grouped<RH_GEMM_NN>(descs, n, g, workspace, st);
+    default: return launch_grouped<RH_GEMM_TN>(descs, n, g, workspace, st);
+  }
+}
+
+extern "C" int rh_gemm_grouped_plan(const rh_gemm_desc* descs, int n, int* splits) {
+  RH_REQUIRE(splits != nullptr && n >= 0 && (n == 0 || descs), "rh_gemm_grouped_plan: bad arguments");
+  for (int i = 0; i < n; ++i) {
+    int rc = validate(&descs[i]);
+    if (rc) return rc;
+  }
+  const GroupPlan g = plan_grouped(descs, n);
+  *splits = g.ok ? g.splits : 0;
+  return RH_OK;
 }

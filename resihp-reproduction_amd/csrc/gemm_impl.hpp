@@ -45,6 +45,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -83,7 +84,21 @@ struct GemmParams {
   int out_vec;          // D/C/aux rows 8-byte aligned, split partials 16-byte aligned
   int epi_lds;          // finish through LDS (epilogue_tile_impl) instead of epilogue_regs
   int tiles_m, tiles_n, group_m;
+  // next-token cross-entropy epilogues of the LM head (kEpiLsePartial, kEpiXentGrad); row m of the
+  // output is token m = b*seq + s, scored against tokens[m + 1] unless s == seq - 1, and output
+  // column n is vocabulary id col_off + n
+  const int64_t* tokens;
+  const float* lse;     // kEpiXentGrad: natural-log log-sum-exp of each row
+  float* part;          // kEpiLsePartial: (max, sum) of each row's 64-column blocks, base-2 units
+  float* tgt;           // kEpiLsePartial: the target logit of each scored row
+  const float* grad;    // kEpiXentGrad: d loss / d mean loss (device scalar)
+  float inv_n;          // 1 / scored rows
+  int64_t seq, col_off, n_store, ld_part;
 };
+
+// Internal epilogues of the fused LM-head cross-entropy (not part of the public RH_EPI_* set).
+constexpr int kEpiLsePartial = 16;
+constexpr int kEpiXentGrad = 17;
 
 template <typename T>
 __device__ __forceinline__ const T* b_row(const GemmParams<T>& p, int64_t r) {
@@ -356,7 +371,7 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
 // used.  Sub-tiles that cross the matrix edge (or unaligned rows) take the per-element path.
 template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int FM, int FN>
 __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, floatx16_t (&acc)[FM][FN], int64_t m0,
-                                              int64_t n0, int wm, int wn, int lane) {
+                                              int64_t n0, int wm, int wn, int lane, int split) {
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   const int64_t wr0 = m0 + (int64_t)wm * WTM, wc0 = n0 + (int64_t)wn * WTN;
   const int g = lane >> 5;
@@ -370,7 +385,7 @@ __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, float
           const int64_t m = wr0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), n = wc0 + j * 32 + (lane & 31);
           if (m >= p.M || n >= p.N) continue;
           if (SPLIT)
-            p.ws[(int64_t)blockIdx.z * p.M * p.N + m * p.N + n] = acc[i][j][r];
+            p.ws[(int64_t)split * p.M * p.N + m * p.N + n] = acc[i][j][r];
           else
             epilogue_store<bf16_t, EPI>(p, m, n, acc[i][j][r]);
         }
@@ -380,7 +395,7 @@ __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, float
   const int64_t rl = wr0 + 4 * g + (lane & 3);
   const int64_t cl = wc0 + (lane & 28);
   if (SPLIT) {
-    float* ws = p.ws + (int64_t)blockIdx.z * p.M * p.N;
+    float* ws = p.ws + (int64_t)split * p.M * p.N;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -483,13 +498,115 @@ __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, float
   }
 }
 
+// LM-head forward without logits: each wave reduces its WTM x 64 sub-tile of logits to one
+// (max, sum of 2^(v log2 e - max)) pair per row in base-2 units, stored at
+// part[m * ld_part + 2 * block] for the row's global 64-column block; the lane holding the row's
+// target column stores that logit (natural units) to tgt[m].  Columns past N take no part.
+template <int BM, int BN, int WGM, int WGN, int FM, int FN>
+__device__ __forceinline__ void epilogue_lse(const GemmParams<bf16_t>& p, floatx16_t (&acc)[FM][FN], int64_t m0,
+                                             int64_t n0, int wm, int wn, int lane) {
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  static_assert(WTN == 64, "the row partials cover 64-column blocks: one per wave");
+  constexpr float kL2e = 1.4426950408889634074f;
+  const int64_t wr0 = m0 + (int64_t)wm * WTM, wc0 = n0 + (int64_t)wn * WTN;
+  const int g = lane >> 5;
+  const int64_t rl = wr0 + 4 * g + (lane & 3);
+  const int64_t cl = wc0 + (lane & 28);
+  const int64_t blk = (p.col_off + wc0) / 64;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = rl + i * 32 + 8 * q;
+      float v[FN][4];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        float t4[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        quad_transpose(t4, lane);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[j][t] = p.alpha * t4[t];
+      }
+      int64_t tc = -1;
+      if (m < p.M && m % p.seq != p.seq - 1) tc = p.tokens[m + 1] - p.col_off;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int64_t n = cl + j * 32 + t;
+          if (n < p.N) mx = fmaxf(mx, v[j][t] * kL2e);
+          if (n == tc) p.tgt[m] = v[j][t];
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      float sum = 0.f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (cl + j * 32 + t < p.N) sum += __builtin_amdgcn_exp2f(fmaf(v[j][t], kL2e, -mx));
+      }
+      sum += __shfl_xor(sum, 4, 64);
+      sum += __shfl_xor(sum, 8, 64);
+      sum += __shfl_xor(sum, 16, 64);
+      if ((lane & 28) == 0 && m < p.M && wc0 < p.N) {
+        p.part[m * p.ld_part + 2 * blk] = mx;
+        p.part[m * p.ld_part + 2 * blk + 1] = sum;
+      }
+    }
+}
+
+// LM-head backward, one vocabulary chunk: the recomputed logits v of row m become
+//   dS = (exp(v - lse[m]) - [col_off + n == target]) * grad * inv_n
+// (0 on the unscored last position of every sequence), stored in bf16 for columns n < N and
+// as zeros for N <= n < n_store (the padding the weight-gradient GEMM reads).
+template <int BM, int BN, int WGM, int WGN, int FM, int FN>
+__device__ __forceinline__ void epilogue_xent_grad(const GemmParams<bf16_t>& p, floatx16_t (&acc)[FM][FN], int64_t m0,
+                                                   int64_t n0, int wm, int wn, int lane) {
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr float kL2e = 1.4426950408889634074f;
+  const int64_t wr0 = m0 + (int64_t)wm * WTM, wc0 = n0 + (int64_t)wn * WTN;
+  const int g = lane >> 5;
+  const int64_t rl = wr0 + 4 * g + (lane & 3);
+  const int64_t cl = wc0 + (lane & 28);
+  const float scale = p.inv_n * *p.grad;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = rl + i * 32 + 8 * q;
+      const bool scored = m < p.M && m % p.seq != p.seq - 1;
+      const int64_t tc = scored ? p.tokens[m + 1] - p.col_off : -1;
+      const float l2 = scored ? p.lse[m] * kL2e : 0.f;
+      bf16_t* drow = m < p.M ? d_row(p, m) : nullptr;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        float t4[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        quad_transpose(t4, lane);
+        const int64_t n = cl + j * 32;
+        if (drow == nullptr || n >= p.n_store) continue;
+        u16x4_t o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float d = 0.f;
+          if (scored && n + t < p.N)
+            d = (__builtin_amdgcn_exp2f(fmaf(p.alpha * t4[t], kL2e, -l2)) - (n + t == tc ? 1.f : 0.f)) * scale;
+          o[t] = f32_to_bf16(d);
+        }
+        *reinterpret_cast<u16x4_t*>(drow + n) = o;
+      }
+    }
+}
+
 // Epilogue through LDS: the fp32 tile is written to LDS in row chunks, then every thread takes
 // 8 consecutive columns at a time -- one rolled loop, 16-byte coalesced loads and stores.
 // 32x32 accumulator: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 // `smem_elems` bf16 elements of LDS are free for it (the caller's stages, after a barrier).
 template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int SMEM_ELEMS, int FM, int FN>
 __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, bf16_t* smem, floatx16_t (&acc)[FM][FN],
-                                                   int64_t m0, int64_t n0, int wm, int wn, int lane) {
+                                                   int64_t m0, int64_t n0, int wm, int wn, int lane, int split) {
   constexpr int NT = 64 * WGM * WGN;
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int CP = BN >= 256 ? BN : BN + 4;                 // fp32 row pitch in LDS
@@ -521,7 +638,7 @@ __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, 
       const floatx4_t hi = *reinterpret_cast<const floatx4_t*>(cs + row * CP + col + 4);
       float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       if (SPLIT) {
-        float* w = p.ws + (int64_t)blockIdx.z * p.M * p.N + m * p.N + n;
+        float* w = p.ws + (int64_t)split * p.M * p.N + m * p.N + n;
         if (n + 8 <= p.N && p.N % 4 == 0) {
           *reinterpret_cast<floatx4_t*>(w) = lo;
           *reinterpret_cast<floatx4_t*>(w + 4) = hi;
@@ -563,15 +680,22 @@ __device__ __forceinline__ void epilogue_tile_impl(const GemmParams<bf16_t>& p, 
 // row runs), the register epilogue for split-K partials and for the aux-reading forms.
 template <int BM, int BN, int WGM, int WGN, int EPI, bool SPLIT, int SMEM_ELEMS, int FM, int FN>
 __device__ __forceinline__ void epilogue_sel(const GemmParams<bf16_t>& p, bf16_t* smem, floatx16_t (&acc)[FM][FN],
-                                             int64_t m0, int64_t n0, int wm, int wn, int lane) {
+                                             int64_t m0, int64_t n0, int wm, int wn, int lane, int split) {
+  if constexpr (EPI == kEpiLsePartial) {
+    epilogue_lse<BM, BN, WGM, WGN>(p, acc, m0, n0, wm, wn, lane);
+    return;
+  } else if constexpr (EPI == kEpiXentGrad) {
+    epilogue_xent_grad<BM, BN, WGM, WGN>(p, acc, m0, n0, wm, wn, lane);
+    return;
+  }
   if constexpr (!SPLIT && !epi_reads_aux<EPI>()) {
     if (p.epi_lds) {
       __syncthreads();  // every wave is done reading the operand stages
-      epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, SMEM_ELEMS>(p, smem, acc, m0, n0, wm, wn, lane);
+      epilogue_tile_impl<BM, BN, WGM, WGN, EPI, SPLIT, SMEM_ELEMS>(p, smem, acc, m0, n0, wm, wn, lane, split);
       return;
     }
   }
-  epilogue_regs<BM, BN, WGM, WGN, EPI, SPLIT>(p, acc, m0, n0, wm, wn, lane);
+  epilogue_regs<BM, BN, WGM, WGN, EPI, SPLIT>(p, acc, m0, n0, wm, wn, lane, split);
 }
 
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
@@ -670,7 +794,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_mfma(GemmParams<bf16
     }
   }
 
-  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane, (int)blockIdx.z);
 }
 
 
@@ -724,8 +848,10 @@ struct DmaOperand {
   }
 };
 
+// One output tile (tm, tn) of split `split` of a direct-to-LDS GEMM, on the workgroup's LDS `smem`
+// (two stages of BM x 64 + BN x 64 bf16).
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_t> p) {
+__device__ __forceinline__ void gemm_dma_tile(const GemmParams<bf16_t>& p, bf16_t* smem, int tm, int tn, int split) {
   constexpr int NW = WGM * WGN;
   constexpr bool A_KC = (L != RH_GEMM_TN);
   constexpr bool B_KC = (L == RH_GEMM_NT);
@@ -733,12 +859,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
   constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK, STAGE = A_ELEMS + B_ELEMS;
   using DA = DmaOperand<BM, A_KC, NW>;
   using DB = DmaOperand<BN, B_KC, NW>;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * STAGE];
 
-  int tm, tn;
-  tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t kbeg = (int64_t)blockIdx.z * p.k_per_split;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
   const int64_t kend = min(p.K, kbeg + p.k_per_split);
   const int nk = (int)((kend - kbeg) / kBK);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -820,7 +943,60 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_
     __syncthreads();
   }
 
-  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane);
+  epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane, split);
+}
+
+template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_t> p) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (BM + BN) * kBK];
+  int tm, tn;
+  tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  gemm_dma_tile<BM, BN, WGM, WGN, L, EPI, SPLIT>(p, smem, tm, tn, (int)blockIdx.z);
+}
+
+// ---------------------------------------------------------------------------
+// Grouped launch: several GEMMs of one layout (the weight gradients of a decoder block, which
+// share the token dimension as K) in ONE grid.  The workgroups are dealt over the problems in a
+// logical order -- problem by problem, split-K slice by slice, tiles in GROUP_M order -- and each
+// XCD takes one contiguous run of it, so the tiles sharing operand panels meet in one L2.
+// ---------------------------------------------------------------------------
+constexpr int kMaxGroup = 4;
+
+struct GroupedParams {
+  GemmParams<bf16_t> p[kMaxGroup];
+  int first[kMaxGroup + 1];  // logical index of each problem's first workgroup (first[count] = total)
+  int splits;
+  int count;
+};
+
+// logical tile t of a tiles_m x tiles_n grid in GROUP_M order
+__device__ __forceinline__ void group_order(int t, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int in = t - g * per_group;
+  tm = first_m + in % gsize;
+  tn = in / gsize;
+}
+
+template <int BM, int BN, int WGM, int WGN, int L, bool SPLIT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_grouped(GroupedParams gp) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (BM + BN) * kBK];
+  const int nwg = gp.first[gp.count];
+  const int bid = blockIdx.x;
+  const int q = nwg / 8, r = nwg % 8;
+  const int xcd = bid % 8, idx = bid / 8;
+  const int logical = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + idx;
+  int i = 0;
+  while (i + 1 < gp.count && logical >= gp.first[i + 1]) ++i;
+  const GemmParams<bf16_t>& p = gp.p[i];
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int local = logical - gp.first[i];
+  const int split = local / tiles;
+  int tm, tn;
+  group_order(local - split * tiles, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  gemm_dma_tile<BM, BN, WGM, WGN, L, RH_EPI_NONE, SPLIT>(p, smem, tm, tn, split);
 }
 
 // ---------------------------------------------------------------------------
@@ -965,6 +1141,13 @@ struct Plan {
 // 256x256 tiles leave a quarter of the CUs idle.
 constexpr double kTileEff[4] = {1.0, 0.85, 0.6, 0.95};
 
+// Cost of one fp32 split-K partial element (written by the main kernel, re-read by the reduce) in
+// the grouped planner's unit (one MAC of a tile's area over k).  Measured on MI355X with a decoder
+// block's four weight gradients (K 8192, 192 tiles of 256x256) in one grouped launch: split 4 (3
+// waves of 2048-deep tiles, 50 M partial elements) takes 270 us against 232 us unsplit (one wave of
+// 8192); ~6 units per element reproduces both.
+constexpr double kGroupSplitCost = 6.0;
+
 inline Plan plan_gemm(const rh_gemm_desc* d) {
   Plan pl{kTf32, 1, 0, 0, 0, 0};
   if (d->dtype != RH_DTYPE_BF16) {
@@ -1005,7 +1188,8 @@ inline Plan plan_gemm(const rh_gemm_desc* d) {
       const int64_t waves = rh_cdiv(tiles * splits, slots);
       double t = (double)waves * per_cu * kShapes[c].bm * kShapes[c].bn * (double)kps / eff;
       // partial write + reduce: measured on MI355X, a split-4 2048x2048 reduce costs ~1/4 of a
-      // 256x256x2048 tile wave, i.e. ~2 units per partial element
+      // 256x256x2048 tile wave, i.e. ~2 units per partial element (the fc2 forward of GPT-2-small,
+      // M 8192 N 768 K 3072, is faster split in two than unsplit on 256x128 tiles)
       if (splits > 1) t += 2.0 * (double)splits * d->M * d->N;
       if (t < best * 0.98) {
         best = t;
@@ -1163,6 +1347,33 @@ void launch_main(int cfg, const GemmParams<T>& p, bool dma, dim3 grid, hipStream
   }
 }
 
+// Sum `slices` fp32 partial slices of p.ws in slice order and apply the epilogue.
+template <typename T, int EPI>
+int launch_reduce(const rh_gemm_desc* d, const GemmParams<T>& p, int slices, const void* ws, hipStream_t st) {
+  const int64_t total = d->M * d->N;
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    // every output row and the partials are 16-byte aligned when N % 8 == 0 (the partials
+    // are [splits][M][N] fp32); D/C/aux rows need ld % 8 == 0 and aligned bases as well
+    bool vec = d->N % 8 == 0 && d->ldd % 8 == 0 && rh_aligned(ws, 16);
+    for (int q = 0; q < d->d_nseg; ++q) vec = vec && rh_aligned(d->D[q], 16);
+    if (d->beta != 0.f && d->C) vec = vec && rh_aligned(d->C, 16) && d->ldc % 8 == 0;
+    if (d->epilogue != RH_EPI_NONE) {
+      const bool writes = d->epilogue == RH_EPI_GELU || d->epilogue == RH_EPI_GELU_DERIV;
+      vec = vec && rh_aligned(writes ? d->aux_out : d->aux, 16) && d->ldaux % 8 == 0;
+    }
+    if (vec) {
+      int64_t blocks = rh_cdiv(total / 8, 256);
+      if (blocks > 8 * 1024) blocks = 8 * 1024;
+      hipLaunchKernelGGL((gemm_splitk_reduce_vec<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
+      return rh_check_launch("rh_gemm split-k reduce");
+    }
+  }
+  int64_t blocks = rh_cdiv(total, 256);
+  if (blocks > 4 * 1024) blocks = 4 * 1024;
+  hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
+  return rh_check_launch("rh_gemm split-k reduce");
+}
+
 template <typename T, int L, int EPI>
 int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t st, int stage) {
   GemmParams<T> p = make_params<T>(d, pl, ws);
@@ -1195,32 +1406,93 @@ int launch_layout(const rh_gemm_desc* d, const Plan& pl, void* ws, hipStream_t s
       }
       if (stage == RH_GEMM_STAGE_MAIN) return RH_OK;
     }
-    const int64_t total = d->M * d->N;
-    if constexpr (std::is_same<T, bf16_t>::value) {
-      // every output row and the partials are 16-byte aligned when N % 8 == 0 (the partials
-      // are [splits][M][N] fp32); D/C/aux rows need ld % 8 == 0 and aligned bases as well
-      bool vec = d->N % 8 == 0 && d->ldd % 8 == 0 && rh_aligned(ws, 16);
-      for (int q = 0; q < d->d_nseg; ++q) vec = vec && rh_aligned(d->D[q], 16);
-      if (d->beta != 0.f && d->C) vec = vec && rh_aligned(d->C, 16) && d->ldc % 8 == 0;
-      if (d->epilogue != RH_EPI_NONE) {
-        const bool writes = d->epilogue == RH_EPI_GELU || d->epilogue == RH_EPI_GELU_DERIV;
-        vec = vec && rh_aligned(writes ? d->aux_out : d->aux, 16) && d->ldaux % 8 == 0;
-      }
-      if (vec) {
-        int64_t blocks = rh_cdiv(total / 8, 256);
-        if (blocks > 8 * 1024) blocks = 8 * 1024;
-        hipLaunchKernelGGL((gemm_splitk_reduce_vec<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
-        return rh_check_launch("rh_gemm split-k reduce");
-      }
-    }
-    int64_t blocks = rh_cdiv(total, 256);
-    if (blocks > 4 * 1024) blocks = 4 * 1024;
-    hipLaunchKernelGGL((gemm_splitk_reduce<T, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, p, slices);
-    return rh_check_launch("rh_gemm split-k reduce");
+    return launch_reduce<T, EPI>(d, p, slices, ws, st);
   }
   if (stage == RH_GEMM_STAGE_REDUCE) return RH_OK;  // unsplit: the main kernel did everything
   launch_main<T, L, EPI, false>(pl.cfg, p, dma, grid, st);
   return rh_check_launch("rh_gemm");
+}
+
+// ---------------------------------------------------------------------------
+// grouped GEMMs (rh_gemm_grouped)
+// ---------------------------------------------------------------------------
+struct GroupPlan {
+  int ok = 0;       // 0: the group runs as separate rh_gemm calls
+  int splits = 1;
+  int64_t kps[kMaxGroup] = {};
+  int64_t ws_off[kMaxGroup + 1] = {};  // byte offset of each problem's partials; ws_off[n] = total
+};
+
+// One launch for the whole group needs bf16, one layout, no epilogue, K a multiple of the k-tile
+// and operands the direct-to-LDS kernel can address; the split-K count (1, 2 or 4, shared by the
+// group) minimises waves x K per split plus the partial traffic, as plan_gemm does.
+inline GroupPlan plan_grouped(const rh_gemm_desc* d, int n) {
+  GroupPlan g;
+  if (n < 1 || n > kMaxGroup) return g;
+  for (int i = 0; i < n; ++i) {
+    if (d[i].dtype != RH_DTYPE_BF16 || d[i].layout != d[0].layout || d[i].epilogue != RH_EPI_NONE) return g;
+    if (d[i].M == 0 || d[i].N == 0 || d[i].K == 0 || d[i].K % kBK) return g;
+  }
+  const int64_t cus = rh_device_cus();
+  double best = 1e300;
+  for (int s : {1, 2, 4}) {
+    int64_t wgs = 0, kmax = 0, partial = 0;
+    bool fits = true;
+    for (int i = 0; i < n; ++i) {
+      const int64_t kps = rh_cdiv(rh_cdiv(d[i].K, s), kBK) * kBK;
+      if (s > 1 && (d[i].K / s < 512 || rh_cdiv(d[i].K, kps) != s)) fits = false;
+      wgs += rh_cdiv(d[i].M, 256) * rh_cdiv(d[i].N, 256) * s;
+      kmax = std::max(kmax, kps);
+      partial += s > 1 ? s * d[i].M * d[i].N : 0;
+    }
+    if (!fits || wgs > INT32_MAX) continue;
+    const double t = (double)rh_cdiv(wgs, cus) * 256.0 * 256.0 * (double)kmax + kGroupSplitCost * (double)partial;
+    if (t < best * 0.98) {
+      best = t;
+      g.splits = s;
+    }
+  }
+  int64_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    Plan pl{kT256x256, g.splits, 0, 0, (int)rh_cdiv(d[i].M, 256), (int)rh_cdiv(d[i].N, 256)};
+    pl.k_per_split = rh_cdiv(rh_cdiv(d[i].K, g.splits), kBK) * kBK;
+    pl.k_main = d[i].K;
+    const GemmParams<bf16_t> p = make_params<bf16_t>(&d[i], pl, nullptr);
+    if (!dma_ok(&d[i], pl, p)) return GroupPlan{};
+    g.kps[i] = pl.k_per_split;
+    g.ws_off[i] = off;
+    if (g.splits > 1) off += rh_cdiv(g.splits * d[i].M * d[i].N * (int64_t)sizeof(float), 256) * 256;
+  }
+  g.ws_off[n] = off;
+  g.ok = 1;
+  return g;
+}
+
+template <int L>
+int launch_grouped(const rh_gemm_desc* d, int n, const GroupPlan& g, void* ws, hipStream_t st) {
+  GroupedParams gp{};
+  int total = 0;
+  for (int i = 0; i < n; ++i) {
+    Plan pl{kT256x256, g.splits, g.kps[i], 0, (int)rh_cdiv(d[i].M, 256), (int)rh_cdiv(d[i].N, 256)};
+    pl.k_main = d[i].K;
+    gp.p[i] = make_params<bf16_t>(&d[i], pl, static_cast<char*>(ws) + g.ws_off[i]);
+    gp.first[i] = total;
+    total += pl.tiles_m * pl.tiles_n * g.splits;
+  }
+  gp.first[n] = total;
+  gp.count = n;
+  gp.splits = g.splits;
+  if (g.splits > 1)
+    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, true>), dim3((unsigned)total), dim3(512), 0, st, gp);
+  else
+    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, false>), dim3((unsigned)total), dim3(512), 0, st, gp);
+  int rc = rh_check_launch("rh_gemm_grouped");
+  if (rc || g.splits == 1) return rc;
+  for (int i = 0; i < n; ++i) {
+    rc = launch_reduce<bf16_t, RH_EPI_NONE>(&d[i], gp.p[i], g.splits, gp.p[i].ws, st);
+    if (rc) return rc;
+  }
+  return RH_OK;
 }
 
 }  // namespace rh_gemm_impl

@@ -14,5 +14,6 @@ template int launch_layout<float, RH_GEMM_NT, RH_EPI_GELU>(const rh_gemm_desc*, 
 template int launch_layout<float, RH_GEMM_NT, RH_EPI_GELU_GRAD>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
 template int launch_layout<float, RH_GEMM_NT, RH_EPI_GELU_DERIV>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
 template int launch_layout<float, RH_GEMM_NT, RH_EPI_MUL_AUX>(const rh_gemm_desc*, const Plan&, void*, hipStream_t, int);
+template int launch_grouped<RH_GEMM_NT>(const rh_gemm_desc*, int, const GroupPlan&, void*, hipStream_t);
 
 }  // namespace rh_gemm_impl

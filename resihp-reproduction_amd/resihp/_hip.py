@@ -103,6 +103,9 @@ _SIGNATURES = {
     "rh_gemm": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_ptr],
     "rh_gemm_stage": [ctypes.POINTER(rh_gemm_desc), c_ptr, c_i64, c_int, c_ptr],
     "rh_gemm_kernel_name": [ctypes.POINTER(rh_gemm_desc), ctypes.c_char_p, c_i64],
+    "rh_gemm_grouped_workspace_bytes": [ctypes.POINTER(rh_gemm_desc), c_int, ctypes.POINTER(c_i64)],
+    "rh_gemm_grouped": [ctypes.POINTER(rh_gemm_desc), c_int, c_ptr, c_i64, c_ptr],
+    "rh_gemm_grouped_plan": [ctypes.POINTER(rh_gemm_desc), c_int, ctypes.POINTER(c_int)],
     "rh_attn_fwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr,
                     c_float, c_int, c_ptr],
     "rh_attn_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],
@@ -127,6 +130,10 @@ _SIGNATURES = {
     "rh_xent_fwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                     c_ptr],
     "rh_xent_bwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr],
+    "rh_lmhead_xent_workspace_bytes": [c_i64, c_i64, c_i64, c_i64, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64)],
+    "rh_lmhead_xent_fwd": [c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr],
+    "rh_lmhead_xent_bwd": [c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_ptr,
+                           c_i64, c_ptr],
     "rh_embedding_fwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr],
     "rh_embedding_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],
     "rh_embedding_bwd": [c_int, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_int, c_ptr, c_i64,

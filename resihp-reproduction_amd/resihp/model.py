@@ -153,6 +153,24 @@ class ReferenceTransformer(nn.Module):
         x = self.final_norm(x)
         return self.lm_head(x)
 
+    def next_token_loss(self, tokens):
+        """``next_token_loss(self(tokens), tokens, vocab_size)`` (resihp/reference.py:41-50) with the LM
+        head fused into the loss, so the [batch, seq, vocab] logits and their gradient never exist
+        (bf16 models; an fp32 model takes the unfused path).  Not in the reference: a memory-saving
+        variant of its forward + loss."""
+        _, seq = tokens.shape
+        if seq != self.sequence_length:
+            raise ValueError("token sequence length does not match the model")
+        if self.lm_head.weight.dtype != torch.bfloat16:
+            from .reference import next_token_loss
+
+            return next_token_loss(self(tokens), tokens, self.vocab_size)
+        x = ops.embedding(tokens, self.token_embedding.weight, self.position_embedding.weight)
+        for gid in self.layer_ids:
+            x = self.layers[str(gid)](x)
+        x = self.final_norm(x)
+        return ops.lm_head_next_token_loss(x, self.lm_head.weight, tokens)
+
     def logical_state_dict(self) -> dict[str, "torch.Tensor"]:
         """Parameters keyed by stable logical name (``layers.<gid>.<...>``)."""
         return {name: param for name, param in self.named_parameters()}

@@ -94,6 +94,30 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
          ldaux: int = 0, b_seg_rows: int = 0, d_seg_rows: int = 0) -> None:
     """One rh_gemm call (see include/resihp_hip.h for the layouts)."""
     dev = H.require_gpu(A, *B, *D, C, aux, aux_out)
+    desc = _gemm_desc(layout, M, N, K, A, lda, B, ldb, D, ldd, alpha=alpha, beta=beta, C=C, ldc=ldc,
+                      epilogue=epilogue, aux=aux, aux_out=aux_out, ldaux=ldaux, b_seg_rows=b_seg_rows,
+                      d_seg_rows=d_seg_rows)
+    nbytes = H.query("rh_gemm_workspace_bytes", ctypes.byref(desc))
+    ws = H.workspace(nbytes, dev)
+    if profiling.active():
+        # main kernel and split-K reduce timed apart (the reduce is a bandwidth kernel)
+        name = ctypes.create_string_buffer(128)
+        H.call("rh_gemm_kernel_name", ctypes.byref(desc), name, 128)
+        with profiling.launch(name.value.decode(), 2.0 * M * N * K):
+            H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_MAIN, H.stream_of(A))
+        if nbytes:
+            # fp32 partials read once; D written, C / aux read or written once (2-byte bf16 storage)
+            es = A.element_size()
+            io = 1 + (beta != 0.0) + (epilogue != H.RH_EPI_NONE)
+            with profiling.launch("gemm_splitk_reduce", 0.0, nbytes + io * M * N * es):
+                H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_REDUCE,
+                       H.stream_of(A))
+        return
+    H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
+
+
+def _gemm_desc(layout, M, N, K, A, lda, B, ldb, D, ldd, *, alpha=1.0, beta=0.0, C=None, ldc=0,
+               epilogue=H.RH_EPI_NONE, aux=None, aux_out=None, ldaux=0, b_seg_rows=0, d_seg_rows=0):
     desc = H.rh_gemm_desc()
     desc.dtype = _same_dtype(A, *B, *D, C, aux, aux_out)
     desc.layout = layout
@@ -118,23 +142,7 @@ def gemm(layout: int, M: int, N: int, K: int, A: torch.Tensor, lda: int, B: list
     desc.aux = None if aux is None else aux.data_ptr()
     desc.aux_out = None if aux_out is None else aux_out.data_ptr()
     desc.ldaux = ldaux
-    nbytes = H.query("rh_gemm_workspace_bytes", ctypes.byref(desc))
-    ws = H.workspace(nbytes, dev)
-    if profiling.active():
-        # main kernel and split-K reduce timed apart (the reduce is a bandwidth kernel)
-        name = ctypes.create_string_buffer(128)
-        H.call("rh_gemm_kernel_name", ctypes.byref(desc), name, 128)
-        with profiling.launch(name.value.decode(), 2.0 * M * N * K):
-            H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_MAIN, H.stream_of(A))
-        if nbytes:
-            # fp32 partials read once; D written, C / aux read or written once (2-byte bf16 storage)
-            es = A.element_size()
-            io = 1 + (beta != 0.0) + (epilogue != H.RH_EPI_NONE)
-            with profiling.launch("gemm_splitk_reduce", 0.0, nbytes + io * M * N * es):
-                H.call("rh_gemm_stage", ctypes.byref(desc), H.ptr(ws), nbytes, H.RH_GEMM_STAGE_REDUCE,
-                       H.stream_of(A))
-        return
-    H.call("rh_gemm", ctypes.byref(desc), H.ptr(ws), nbytes, H.stream_of(A))
+    return desc
 
 
 def linear_fwd(x2: torch.Tensor, ws: list, *, residual: torch.Tensor | None = None,
@@ -172,11 +180,13 @@ def linear_dgrad(dy2: torch.Tensor, ws: list, *, gelu_pre: torch.Tensor | None =
     return dx
 
 
-def linear_wgrad(dy2: torch.Tensor, x2: torch.Tensor, params: list) -> None:
-    """param.grad (+)= dy^T . x, with dy's columns split over ``params`` (rows of W)."""
+def _wgrad_setup(dy2: torch.Tensor, x2: torch.Tensor, params: list, allow_pad: bool = True):
+    """The TN GEMM of param.grad (+)= dy^T . x (dy's columns split over ``params``, rows of W):
+    (desc, finish) with ``finish()`` folding any side buffer into .grad, or None when no
+    parameter wants a gradient."""
     want = [_wants(p) for p in params]
     if not any(want):
-        return
+        return None
     M_rows, N_out = dy2.shape
     K_in = x2.shape[1]
     seg = params[0].shape[0]
@@ -193,7 +203,8 @@ def linear_wgrad(dy2: torch.Tensor, x2: torch.Tensor, params: list) -> None:
         accs = [True] * len(accs)
     M_gemm, d_seg = N_out, (seg if len(params) > 1 else 0)
     pad_rows = -N_out % 8
-    if (len(params) == 1 and pad_rows and dy2.dtype == torch.bfloat16 and _ld(dy2) >= N_out + pad_rows
+    if (allow_pad and len(params) == 1 and pad_rows and dy2.dtype == torch.bfloat16
+            and _ld(dy2) >= N_out + pad_rows
             and dy2.storage_offset() + (M_rows - 1) * _ld(dy2) + N_out + pad_rows
             <= dy2.untyped_storage().nbytes() // dy2.element_size()):
         # A ragged output count (the LM head's vocabulary, 50257) keeps the m-contiguous dy off the
@@ -202,11 +213,54 @@ def linear_wgrad(dy2: torch.Tensor, x2: torch.Tensor, params: list) -> None:
         # land in a scratch segment and are dropped.
         M_gemm, d_seg = N_out + pad_rows, N_out
         targets = targets + [torch.empty(pad_rows, K_in, dtype=targets[0].dtype, device=targets[0].device)]
-    gemm(H.RH_GEMM_TN, M_gemm, K_in, M_rows, dy2, _ld(dy2), [x2], _ld(x2), targets, K_in,
-         beta=1.0 if accs[0] else 0.0, d_seg_rows=d_seg)
-    for p, buf, w in zip(params, targets, want):
-        if w:
-            _finish_grad(p, buf)
+    desc = _gemm_desc(H.RH_GEMM_TN, M_gemm, K_in, M_rows, dy2, _ld(dy2), [x2], _ld(x2), targets, K_in,
+                      beta=1.0 if accs[0] else 0.0, d_seg_rows=d_seg)
+
+    def finish():
+        for p, buf, w in zip(params, targets, want):
+            if w:
+                _finish_grad(p, buf)
+
+    return desc, finish, (dy2, x2, targets)
+
+
+def linear_wgrad(dy2: torch.Tensor, x2: torch.Tensor, params: list) -> None:
+    """param.grad (+)= dy^T . x, with dy's columns split over ``params`` (rows of W)."""
+    setup = _wgrad_setup(dy2, x2, params)
+    if setup is None:
+        return
+    desc, finish, keep = setup
+    d = desc
+    targets = keep[2]
+    gemm(H.RH_GEMM_TN, d.M, d.N, d.K, dy2, d.lda, [x2], d.ldb, targets, d.ldd, beta=d.beta,
+         d_seg_rows=d.d_seg_rows)
+    finish()
+
+
+def linear_wgrad_group(items: list) -> None:
+    """Several weight gradients -- [(dy2, x2, params)], at most 4 -- as ONE grouped GEMM launch
+    (rh_gemm_grouped): the wgrads of a decoder block share the token count as K and together fill
+    the chip, so none of them needs a split-K pass of its own."""
+    setups = [s for s in (_wgrad_setup(dy2, x2, ps, allow_pad=False) for dy2, x2, ps in items) if s is not None]
+    if not setups:
+        return
+    descs = (H.rh_gemm_desc * len(setups))(*[s[0] for s in setups])
+    dev = setups[0][2][0].device
+    nbytes = H.query("rh_gemm_grouped_workspace_bytes", descs, len(setups))
+    ws = H.workspace(nbytes, dev)
+    stream = H.stream_of(setups[0][2][0])
+    if profiling.active():
+        splits = ctypes.c_int(0)
+        H.call("rh_gemm_grouped_plan", descs, len(setups), ctypes.byref(splits))
+        flops = sum(2.0 * s[0].M * s[0].N * s[0].K for s in setups)
+        label = (f"gemm_bf16_dma_grouped<256, 256, 2, 4, 2, {'true' if splits.value > 1 else 'false'}>"
+                 + (" + split-K reduce" if splits.value > 1 else "")) if splits.value else "gemm (group as single calls)"
+        with profiling.launch(label, flops):
+            H.call("rh_gemm_grouped", descs, len(setups), H.ptr(ws), nbytes, stream)
+    else:
+        H.call("rh_gemm_grouped", descs, len(setups), H.ptr(ws), nbytes, stream)
+    for s in setups:
+        s[1]()
 
 
 # ---------------------------------------------------------------------------
@@ -322,13 +376,6 @@ def _attention_forward(n1, wq, wk, wv, num_heads, batch, seq):
     qkv = linear_fwd(n1, [wq, wk, wv])
     ctx, lse, ctx_lo = attn_fwd(qkv, batch, seq, num_heads, head_dim)
     return qkv, ctx, lse, ctx_lo, head_dim
-
-
-def _attention_backward(dctx, n1, qkv, ctx, lse, ctx_lo, wq, wk, wv, num_heads, head_dim, batch, seq, need_dx=True):
-    dqkv = attn_bwd(dctx, qkv, ctx, lse, batch, seq, num_heads, head_dim, ctx_lo)
-    dn1 = linear_dgrad(dqkv, [wq, wk, wv]) if need_dx else None
-    linear_wgrad(dqkv, n1, [wq, wk, wv])
-    return dn1
 
 
 # ---------------------------------------------------------------------------
@@ -462,9 +509,9 @@ class _AttentionFn(torch.autograd.Function):
         batch, seq, num_heads, head_dim = ctx.meta
         dout2 = _as_rows(dout).contiguous()
         dctx = linear_dgrad(dout2, [wo])
-        linear_wgrad(dout2, c, [wo])
-        dx = _attention_backward(dctx, x2, qkv, c, lse, c_lo, wq, wk, wv, num_heads, head_dim, batch, seq,
-                                 need_dx=ctx.needs_input_grad[0])
+        dqkv = attn_bwd(dctx, qkv, c, lse, batch, seq, num_heads, head_dim, c_lo)
+        dx = linear_dgrad(dqkv, [wq, wk, wv]) if ctx.needs_input_grad[0] else None
+        linear_wgrad_group([(dout2, c, [wo]), (dqkv, x2, [wq, wk, wv])])
         return (dx.view(batch, seq, -1) if dx is not None else None), None, None, None, None, None
 
 
@@ -490,9 +537,8 @@ class _MLPFn(torch.autograd.Function):
         w1, w2 = ctx.params
         dy2 = _as_rows(dy).contiguous()
         du = linear_dgrad(dy2, [w2], gelu_deriv=gd)
-        linear_wgrad(dy2, h, [w2])
         dx = linear_dgrad(du, [w1]) if ctx.needs_input_grad[0] else None
-        linear_wgrad(du, x2, [w1])
+        linear_wgrad_group([(dy2, h, [w2]), (du, x2, [w1])])
         return (dx.view(ctx.shape) if dx is not None else None), None, None
 
 
@@ -530,17 +576,16 @@ class _BlockFn(torch.autograd.Function):
         g1, b1, wq, wk, wv, wo, g2, b2, w1, w2 = ctx.params
         batch, seq, num_heads, head_dim = ctx.meta
         d2 = _as_rows(dout).contiguous()
-        # MLP branch
+        # the chain of input gradients first: MLP branch, then the attention branch
         du = linear_dgrad(d2, [w2], gelu_deriv=gd)
-        linear_wgrad(d2, h, [w2])
         dn2 = linear_dgrad(du, [w1])
-        linear_wgrad(du, n2, [w1])
         dx1 = ln_bwd(dn2, x1, mu2, rs2, g2, b2, dres=d2)
-        # attention branch
         dctx = linear_dgrad(dx1, [wo])
-        linear_wgrad(dx1, c, [wo])
-        dn1 = _attention_backward(dctx, n1, qkv, c, lse, c_lo, wq, wk, wv, num_heads, head_dim, batch, seq)
+        dqkv = attn_bwd(dctx, qkv, c, lse, batch, seq, num_heads, head_dim, c_lo)
+        dn1 = linear_dgrad(dqkv, [wq, wk, wv])
         dx = ln_bwd(dn1, x2, mu1, rs1, g1, b1, dres=dx1)
+        # then the block's four weight gradients (token count as K) in one grouped launch
+        linear_wgrad_group([(d2, h, [w2]), (du, n2, [w1]), (dx1, c, [wo]), (dqkv, n1, [wq, wk, wv])])
         return (dx.view(batch, seq, -1),) + (None,) * 12
 
 
@@ -601,6 +646,63 @@ class _NextTokenLossFn(torch.autograd.Function):
         return dl.view(batch, seq, dl.shape[1])[:, :, :vocab], None, None
 
 
+class _LMHeadNextTokenLossFn(torch.autograd.Function):
+    """lm_head then next_token_loss, fused (resihp/model.py:116,133 + resihp/reference.py:41-50):
+    the loss from x [B, S, d] (the final LayerNorm's output) and W [V, d] without the [B, S, V]
+    logits or their gradient in memory.  Backward returns dx and writes W.grad (accumulating,
+    like the other parameters)."""
+
+    @staticmethod
+    def forward(ctx, x, w, tokens):
+        H.require_gpu(x, w, tokens)
+        if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+            raise TypeError("the fused LM-head loss runs in bfloat16")
+        if tokens.dtype != torch.int64:
+            raise TypeError("token ids must be int64")
+        batch, seq, dim = x.shape
+        if tokens.shape != (batch, seq):
+            raise ValueError("tokens must be [batch, seq] matching the hidden states")
+        vocab = w.shape[0]
+        if w.shape[1] != dim:
+            raise ValueError(f"LM head of width {w.shape[1]} applied to hidden states of width {dim}")
+        x2 = _as_rows(x).contiguous()
+        wc = w.contiguous()
+        tokens = tokens.contiguous()
+        fwd_b = ctypes.c_int64(0)
+        bwd_b = ctypes.c_int64(0)
+        H.call("rh_lmhead_xent_workspace_bytes", batch, seq, vocab, dim, ctypes.byref(fwd_b), ctypes.byref(bwd_b))
+        ws = H.workspace(fwd_b.value, x.device)
+        lse = torch.empty(batch * seq, dtype=torch.float32, device=x.device)
+        loss = torch.empty((), dtype=torch.float32, device=x.device)
+        with profiling.launch("lmhead_xent_fwd (LSE GEMM + combine)", 2.0 * batch * seq * vocab * dim):
+            H.call("rh_lmhead_xent_fwd", batch, seq, vocab, dim, x2.data_ptr(), wc.data_ptr(), tokens.data_ptr(),
+                   lse.data_ptr(), loss.data_ptr(), H.ptr(ws), fwd_b.value, H.stream_of(x))
+        ctx.save_for_backward(x2, tokens, lse)
+        ctx.w = w
+        ctx.meta = (batch, seq, vocab, dim, bwd_b.value)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad):
+        x2, tokens, lse = ctx.saved_tensors
+        w = ctx.w
+        batch, seq, vocab, dim, nbytes = ctx.meta
+        grad = grad.to(torch.float32).contiguous()
+        dx = torch.empty_like(x2)
+        if _wants(w):
+            gw, acc = _grad_target(w)
+        else:
+            gw, acc = torch.empty_like(w, memory_format=torch.contiguous_format), False
+        ws = H.workspace(nbytes, x2.device)
+        with profiling.launch("lmhead_xent_bwd (recompute + dW + dX, chunked)", 3 * 2.0 * batch * seq * vocab * dim):
+            H.call("rh_lmhead_xent_bwd", batch, seq, vocab, dim, x2.data_ptr(), w.contiguous().data_ptr(),
+                   tokens.data_ptr(), lse.data_ptr(), grad.data_ptr(), dx.data_ptr(), gw.data_ptr(), 1 if acc else 0,
+                   H.ptr(ws), nbytes, H.stream_of(x2))
+        if _wants(w):
+            _finish_grad(w, gw)
+        return dx.view(batch, seq, dim), None, None
+
+
 # ---------------------------------------------------------------------------
 # functional entry points
 # ---------------------------------------------------------------------------
@@ -632,3 +734,8 @@ def transformer_block(x, g1, b1, wq, wk, wv, wo, g2, b2, w1, w2, num_heads: int,
 
 def next_token_loss(logits: torch.Tensor, tokens: torch.Tensor, vocab_size: int) -> torch.Tensor:
     return _NextTokenLossFn.apply(logits, tokens, vocab_size)
+
+
+def lm_head_next_token_loss(x: torch.Tensor, weight: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """next_token_loss(F.linear(x, weight), tokens, V) without materialising the logits (bf16)."""
+    return _LMHeadNextTokenLossFn.apply(x, weight, tokens)

@@ -537,3 +537,81 @@ def test_embedding_backward_any_token_count(cuda, dtype, batch, seq, vocab, repe
     W.grad = None
     ops.embedding(tokens, W).backward(dout)
     assert torch.equal(W.grad, first)
+
+
+def _wgrad_desc(dy, x, D, beta, d_seg=0):
+    """TN descriptor of D (+)= dy^T . x (D a list of row segments)."""
+    return ops._gemm_desc(H.RH_GEMM_TN, dy.shape[1], x.shape[1], dy.shape[0], dy, dy.stride(0), [x], x.stride(0), D,
+                          x.shape[1], beta=beta, d_seg_rows=d_seg)
+
+
+@pytest.mark.parametrize("shapes,want_splits", [
+    # one TP=4 rank of the 1.3B block: fc2, fc1, out_proj, q|k|v (K = 8192 tokens)
+    ([(2048, 2048), (2048, 2048), (2048, 512), (1536, 2048)], None),
+    # GPT-2-small's block (d 768, FFN 3072): too few tiles alone, so K is split
+    ([(768, 3072), (3072, 768), (768, 768), (2304, 768)], 2),
+    ([(256, 512)], None),
+])
+def test_gemm_grouped_weight_gradients(cuda, shapes, want_splits):
+    """rh_gemm_grouped over a block's weight gradients (dW = dy^T x, K = tokens): every problem
+    equals its fp32 product within bf16 rounding, accumulates into existing gradients (beta 1), writes
+    three q|k|v row segments, and agrees with separate rh_gemm calls; the plan uses the expected
+    split count."""
+    T = 8192
+    descs, outs, refs, keep = [], [], [], []
+    for i, (m, n) in enumerate(shapes):
+        dy = _rand(T, m, seed=100 + i, scale=0.1)
+        x = _rand(T, n, seed=200 + i)
+        prev = _rand(m, n, seed=300 + i)
+        ref = dy.float().t() @ x.float() + prev.float()
+        if i == 3:  # q|k|v: three row segments of m/3
+            segs = [prev[j * m // 3:(j + 1) * m // 3].clone() for j in range(3)]
+            descs.append(_wgrad_desc(dy, x, segs, 1.0, d_seg=m // 3))
+            outs.append(segs)
+        else:
+            D = prev.clone()
+            descs.append(_wgrad_desc(dy, x, [D], 1.0))
+            outs.append([D])
+        refs.append(ref)
+        keep += [dy, x]
+    arr = (H.rh_gemm_desc * len(descs))(*descs)
+    splits = ctypes.c_int(-1)
+    H.call("rh_gemm_grouped_plan", arr, len(descs), ctypes.byref(splits))
+    assert splits.value >= 1  # one launch for the whole group
+    if want_splits is not None:
+        assert splits.value == want_splits
+    nbytes = H.query("rh_gemm_grouped_workspace_bytes", arr, len(descs))
+    ws = H.workspace(nbytes, torch.device(cuda))
+    H.call("rh_gemm_grouped", arr, len(descs), H.ptr(ws), nbytes, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for i, (o, ref) in enumerate(zip(outs, refs)):
+        got = torch.cat(o, 0)
+        assert rel_inf(got, ref) <= BF16_TOL, (i, rel_inf(got, ref))
+    # separate calls on the same inputs agree to within the bf16 rounding of two summation orders
+    for i, (m, n) in enumerate(shapes):
+        dy, x = keep[2 * i], keep[2 * i + 1]
+        D = torch.zeros(m, n, dtype=torch.bfloat16, device=cuda)
+        ops.gemm(H.RH_GEMM_TN, m, n, T, dy, m, [x], n, [D], n)
+        assert rel_inf(torch.cat(outs[i], 0).float() - (refs[i] - dy.float().t() @ x.float()), D) <= BF16_TOL
+
+
+def test_gemm_grouped_falls_back_for_mixed_groups(cuda):
+    """A group the single launch cannot take (an fp32 problem, a ragged K) runs as consecutive
+    rh_gemm calls with the same results."""
+    a32, b32 = _rand(100, 48, dtype=torch.float32, seed=1), _rand(100, 40, dtype=torch.float32, seed=2)
+    D32 = torch.zeros(48, 40, device=cuda)
+    abf, bbf = _rand(96, 64, seed=3), _rand(96, 128, seed=4)
+    Dbf = torch.zeros(64, 128, dtype=torch.bfloat16, device=cuda)
+    for descs, outs in (([_wgrad_desc(a32, b32, [D32], 0.0)], [(D32, a32, b32)]),
+                        ([_wgrad_desc(abf, bbf, [Dbf], 0.0)], [(Dbf, abf, bbf)])):
+        arr = (H.rh_gemm_desc * len(descs))(*descs)
+        splits = ctypes.c_int(-1)
+        H.call("rh_gemm_grouped_plan", arr, len(descs), ctypes.byref(splits))
+        assert splits.value == 0
+        nbytes = H.query("rh_gemm_grouped_workspace_bytes", arr, len(descs))
+        ws = H.workspace(nbytes, torch.device(cuda))
+        H.call("rh_gemm_grouped", arr, len(descs), H.ptr(ws), nbytes, None)
+        torch.cuda.synchronize()
+        for D, a, b in outs:
+            tol = F32_TOL if D.dtype == torch.float32 else BF16_TOL
+            assert rel_inf(D, a.float().t() @ b.float()) <= tol

@@ -368,3 +368,49 @@ def test_pp_boundary_slabs_are_bit_exact(cuda, up, down):
         rebuilt = boundary.reconstruct([slabs[r] for r in receivers], t.shape)
         assert torch.equal(rebuilt.cpu(), t)
         assert torch.equal(torch_ref.boundary_reconstruct([slabs[r].cpu() for r in receivers], t.shape), t)
+
+
+def test_fused_lm_head_loss_matches_fp32_oracle(cuda):
+    """GPT-2-small at full size through the fused LM head + cross-entropy (no logits tensor, vocabulary
+    50257 recomputed in 8192-id chunks in the backward): loss and every gradient within 2e-2 of the
+    fp32 oracle, and within bf16 noise of the unfused bf16 path; gradients accumulate."""
+    d, layers, heads, vocab, seq, batch = 768, 12, 12, 50257, 1024, 8
+    st, model, tokens = _bf16_case(cuda, d=d, heads=heads, layers=layers, vocab=vocab, seq=seq, batch=batch, seed=17)
+    tok = tokens.to(cuda)
+    loss = model.next_token_loss(tok)
+    loss.backward()
+    fused = {n: p.grad.clone() for n, p in model.named_parameters()}
+    ref_logits, ref_loss, ref_grads = torch_ref.loss_and_grads({k: v.to(cuda) for k, v in st.items()}, tok, heads,
+                                                               range(layers), vocab)
+    del ref_logits
+    errs = {"loss": abs(float(loss) - float(ref_loss)) / abs(float(ref_loss))}
+    for name in fused:
+        errs[name] = rel_inf(fused[name], ref_grads[name])
+    worst = max(errs, key=errs.get)
+    print(f"fused LM head: loss {float(loss):.6f} vs {float(ref_loss):.6f}, worst {worst} {errs[worst]:.2e}")
+    for name, err in errs.items():
+        assert err <= 2e-2, (name, err)
+    # a second backward accumulates into .grad like the unfused path
+    model.next_token_loss(tok).backward()
+    assert rel_inf(model.lm_head.weight.grad, 2 * fused["lm_head.weight"]) <= 1e-2
+
+
+@pytest.mark.parametrize("batch,seq,vocab,dim", [(2, 64, 1000, 128), (3, 33, 20000, 64), (1, 256, 8192, 192)])
+def test_fused_lm_head_loss_small(cuda, batch, seq, vocab, dim):
+    """Ragged vocabularies (one chunk, several chunks, exactly one chunk), odd sequence lengths and a
+    grad_loss != 1: the fused head against the fp32 oracle (F.linear + next-token cross-entropy)."""
+    g = torch.Generator().manual_seed(vocab)
+    x = (torch.randn(batch, seq, dim, generator=g)).to(torch.bfloat16)
+    w = (torch.randn(vocab, dim, generator=g) * 0.05).to(torch.bfloat16)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g)
+    xg = x.to(cuda).requires_grad_(True)
+    wg = torch.nn.Parameter(w.to(cuda))
+    loss = ops.lm_head_next_token_loss(xg, wg, tokens.to(cuda))
+    (loss * 0.5).backward()
+    xr = x.to(cuda).float().requires_grad_(True)
+    wr = w.to(cuda).float().requires_grad_(True)
+    ref = torch_ref.next_token_loss(torch.nn.functional.linear(xr, wr), tokens.to(cuda), vocab)
+    (ref * 0.5).backward()
+    assert abs(float(loss) - float(ref)) <= 2e-2 * abs(float(ref))
+    assert rel_inf(xg.grad, xr.grad) <= 2e-2
+    assert rel_inf(wg.grad, wr.grad) <= 2e-2
