@@ -358,9 +358,13 @@ struct FragAddr {
 // Operand fragment of rows r0 + lane%32 (r0 a multiple of 16), eight columns 16*ks + 8*(lane/32)
 // (ds_read_b128).  `tile` is 256-byte aligned.
 template <int D>
-__device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int ks, const FragAddr<D>& fa) {
-  const uint32_t a = (lds_addr(tile) + (uint32_t)(2 * D * r0) + fa.row) ^ (uint32_t)(32 * ks);
+__device__ __forceinline__ bf16x8_t row_frag_at(uint32_t tile, int r0, int ks, const FragAddr<D>& fa) {
+  const uint32_t a = (tile + (uint32_t)(2 * D * r0) + fa.row) ^ (uint32_t)(32 * ks);
   return *(const __attribute__((address_space(3))) bf16x8_t*)(uintptr_t)a;
+}
+template <int D>
+__device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int ks, const FragAddr<D>& fa) {
+  return row_frag_at<D>(lds_addr(tile), r0, ks, fa);
 }
 
 // Transposed operand fragment: rows of the MFMA operand are the 32 tile columns 32*db..+31,
@@ -369,8 +373,8 @@ __device__ __forceinline__ bf16x8_t row_frag(const bf16_t* tile, int r0, int ks,
 // lane i addresses tile row r0 + 4g + i/4 (+8), columns 32*db + 16*(block&1) + 4*(i%4)..+3,
 // and lane j receives those four rows of column 32*db + 16*(block&1) + j.
 template <int D>
-__device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int db, const FragAddr<D>& fa) {
-  const uint32_t base = lds_addr(tile) + (uint32_t)(2 * D * r0);
+__device__ __forceinline__ bf16x8_t tr_frag_at(uint32_t tile, int r0, int db, const FragAddr<D>& fa) {
+  const uint32_t base = tile + (uint32_t)(2 * D * r0);
   const uint32_t a0 = (base + fa.tr[0]) ^ (uint32_t)(64 * db);
   const uint32_t a1 = (base + fa.tr[1]) ^ (uint32_t)(64 * db);
   const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(uintptr_t)a0);
@@ -378,6 +382,41 @@ __device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int db, 
   s16x4_t both[2] = {lo, hi};
   return __builtin_bit_cast(bf16x8_t, both);
 }
+template <int D>
+__device__ __forceinline__ bf16x8_t tr_frag(const bf16_t* tile, int r0, int db, const FragAddr<D>& fa) {
+  return tr_frag_at<D>(lds_addr(tile), r0, db, fa);
+}
+
+// Every fragment address a wave reads from one 32-row block of a stage slot, precomputed per
+// lane: the XOR constant of the k-step / head-dim block and the wave's row block are folded into
+// one register per read pattern, so a read is a single ds_read whose immediate offset carries
+// the stage slot (and the 16-row half of a transposed read).  Valid because tile slots and row
+// blocks are multiples of 2*D*32 bytes and the swizzled in-block offsets stay below that.
+template <int D>
+struct BlockFrags {
+  uint32_t row[D / 16];    // row fragment of k-step ks
+  uint32_t tr[D / 32][2];  // transposed fragment of head-dim block db, lo / hi read
+  __device__ __forceinline__ BlockFrags(const FragAddr<D>& fa, uint32_t block_base) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) row[ks] = block_base + (fa.row ^ (uint32_t)(32 * ks));
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) tr[db][h] = block_base + (fa.tr[h] ^ (uint32_t)(64 * db));
+  }
+  // row fragment ks of the block at byte offset `slot` (a compile-time constant in the callers)
+  __device__ __forceinline__ bf16x8_t rowf(uint32_t slot, int ks) const {
+    return *(const __attribute__((address_space(3))) bf16x8_t*)(uintptr_t)(row[ks] + slot);
+  }
+  // transposed fragment db of rows 16*half.. of the block at byte offset `slot`
+  __device__ __forceinline__ bf16x8_t trf(uint32_t slot, int half, int db) const {
+    const uint32_t o = slot + (uint32_t)(2 * D * 16 * half);
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(uintptr_t)(tr[db][0] + o));
+    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(uintptr_t)(tr[db][1] + o));
+    s16x4_t both[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8_t, both);
+  }
+};
 
 // ROWS rows x D of a [token][ld] bf16 matrix (rows r0.., clamped to `last`) into a swizzled
 // LDS tile with direct global->LDS loads.  Each wave fills whole 1 KB windows of the tile: lane
@@ -410,6 +449,25 @@ struct RowDma {
   __device__ __forceinline__ RowDma(int64_t ld_, int wave, int lane) : ld(ld_) {
     const int row = wave * RPW + lane / CPR;
     off = (uint32_t)(2 * (int64_t)(lane / CPR) * ld + 16 * sw_chunk(row, lane % CPR));
+  }
+  // The same load with the tile given as an LDS byte address; the stage's first row of this
+  // wave is formed once and each further window is a fixed byte stride from it.
+  __device__ __forceinline__ void issue(uint32_t tile, const bf16_t* base, int r0, int last, int wave,
+                                        int lane) const {
+    if (r0 + ROWS - 1 <= last) {
+      const char* g = reinterpret_cast<const char*>(base + ((int64_t)r0 + wave * RPW) * ld);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) dma16s(g + (int64_t)i * (16 * RPW) * ld, off, tile + (uint32_t)((wave + 8 * i) * 1024));
+    } else {
+      const bf16_t* sb = base + (int64_t)r0 * ld;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int row = (wave + 8 * i) * RPW + lane / CPR;
+        const int grow = max(min(row, last - r0), 0);
+        dma16s(sb, (uint32_t)(2 * (int64_t)grow * ld + 16 * sw_chunk(row, lane % CPR)),
+               tile + (uint32_t)((wave + 8 * i) * 1024));
+      }
+    }
   }
   __device__ __forceinline__ void issue(bf16_t* tile, const bf16_t* base, int r0, int last, int wave,
                                         int lane) const {
@@ -521,18 +579,68 @@ __device__ __forceinline__ void merge_phases(float* cbuf, floatx16_t (&acc)[N], 
   __syncthreads();
 }
 
+// Row max of a 32x32 score tile (registers of the lane plus lane ^ 32), times the log2 scale.
+__device__ __forceinline__ float tile_row_max(const floatx16_t& s, float c) {
+  float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])), fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+  const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
+                                                   false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1])) * c;
+}
+
+// Lazy rescaling of the forward's running state: keep the running max m while no row's max grows
+// by more than 8 (so every p = 2^(s*c - m) stays <= 256, far inside fp32 and bf16 range); the
+// final division by the row sum makes the result independent of which max was used.
+template <int DB>
+__device__ __forceinline__ void lazy_rescale(float mx, floatx16_t (&oacc)[DB], float& m, float& lsum) {
+  if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+    const float mnew = fmaxf(m, mx);
+    const float corr = __builtin_amdgcn_exp2f(m - mnew);
+    lsum *= corr;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+    m = mnew;
+  }
+}
+
+// Forward.  Per wave and stage: Sᵀ = K·Qᵀ for the wave's 32 keys x 32 queries, online softmax,
+// Oᵀ += Vᵀ·Pᵀ.
+//  * Software pipeline across stages: the MFMAs of stage t+1's scores are interleaved, one by
+//    one, with the exponentials of stage t's scores, and stage t's Oᵀ MFMAs follow; so the
+//    matrix core and the VALU work side by side within each wave.  K therefore runs one stage
+//    ahead of V: at the top of iteration t the LDS holds K(t+1) and V(t), and K(t+2) / V(t+1)
+//    are loaded into the slots that K(t) / V(t-1) left (two slots per operand).
+//  * Every fragment is read from LDS two MFMAs before its use (scheduling barriers keep that
+//    order), so LDS latency is covered by the preceding MFMAs.
+//  * Loads are explicit saddr direct-to-LDS loads (one offset register serves K and V, which
+//    share a leading dimension), issued right after the barrier that frees their slot and
+//    awaited just before the next one.
+//  * Only the last stage of an item can hold masked keys (the causal diagonal, keys past S), so
+//    every earlier stage runs one branch-free body; the loop takes two stages per trip so the
+//    two score tiles swap roles without register copies.
+//  * The 4 phases' partial outputs are merged by all 8 waves: each wave scales its partial by
+//    its share of the row normaliser, writes it to LDS, and then sums (in phase order) and
+//    stores 8 whole rows of the output with 16-byte row-contiguous stores.
 template <int D>
 __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nitems) {
-  constexpr int KS = D / 16, DB = D / 32, TILE = kStageRows * D;
-  __shared__ __attribute__((aligned(256))) bf16_t smem[2 * 2 * TILE];  // 2 stages x (K, V)
-  static_assert((6 * DB * 16 * 64 + 1024) * 4 <= 2 * 2 * TILE * 2, "merge buffer must fit the stages");
+  constexpr int KS = D / 16, DB = D / 32, NPV = 2 * DB, TILE = kStageRows * D;
+  constexpr int EPS = 16 / KS;       // scores exponentiated per score MFMA
+  constexpr uint32_t TB = 2 * TILE;  // bytes per tile
+  __shared__ __attribute__((aligned(256))) bf16_t smem[4 * TILE];  // K slots 0, 1 then V slots 0, 1
+  __shared__ float mbuf[2][kPhases][2][64];                         // m and lsum of every wave
+  static_assert(kPhases * 64 * D * 4 <= 4 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in an SGPR
   const int sub = w & 1, ph = w >> 1;
   const FragAddr<D> fa(lane);
+  const RowDma<D> dma(a.ld_qkv, w, lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
-  float* cbuf = reinterpret_cast<float*>(smem);
+  const uint32_t ks0 = lds_addr(smem), vs0 = ks0 + 2 * TB;
+  // K fragments: the wave's 32 keys of a K slot; V fragments: the same keys of a V slot
+  const BlockFrags<D> kf(fa, ks0 + (uint32_t)(2 * D * 32 * ph)), vf(fa, vs0 + (uint32_t)(2 * D * 32 * ph));
 
   for (int pass = 0; pass < 2; ++pass) {
     const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
@@ -541,121 +649,166 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
     const int b = it.bh / H, h = it.bh % H;
     const int64_t tok0 = (int64_t)b * S;
     const int wq0 = it.blk * 64 + 32 * sub, wq1 = wq0 + 31, q_row = wq0 + l32;
-
-    bf16x8_t qreg[KS];
-    load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, q_row < S, g);
-    floatx16_t oacc[DB];
-#pragma unroll
-    for (int d = 0; d < DB; ++d) oacc[d] = zero16();
-    float m = -INFINITY, lsum = 0.f;
-
     const bf16_t* kbase = a.k + tok0 * a.ld_qkv + (int64_t)h * D;
     const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
     const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
     const int nst = (kv_end + kStageRows - 1) / kStageRows;
-    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
-    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
-    wait_vm();
+
+    bf16x8_t qreg[KS];
+    load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, q_row < S, g);
+    dma.issue(ks0, kbase, 0, S - 1, w, lane);
+    dma.issue(vs0, vbase, 0, S - 1, w, lane);
+    if (nst > 1) {
+      dma.issue(ks0 + TB, kbase, kStageRows, S - 1, w, lane);
+      wait_vm_le<2 * RowDma<D>::PER>();  // K(0) landed; V(0), K(1) may still be in flight
+    } else {
+      wait_vm_le<RowDma<D>::PER>();
+    }
     __syncthreads();
-    for (int t = 0; t < nst; ++t) {
-      if (t + 1 < nst) {
-        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-        dma_rows<D>(nxt, kbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
-        dma_rows<D>(nxt + TILE, vbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
+    floatx16_t oacc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) oacc[d] = zero16();
+    float m = -INFINITY, lsum = 0.f;
+    // scores of the wave's block of stage 0 (computed whether or not the block is masked: the
+    // last stage masks or skips it) and their row max
+    floatx16_t sa = zero16(), sb;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) sa = mfma32(kf.rowf(0, i), qreg[i], sa);
+    float mxc = tile_row_max(sa, c);
+
+    // One interior stage t (parity par = t & 1): every key of the wave's block precedes every
+    // query of the wave, so nothing is masked.  `cur` holds stage t's scores (row max mxc) and
+    // becomes its probabilities; `nxt` receives stage t+1's scores and mxc their row max.
+    auto interior = [&](floatx16_t& cur, floatx16_t& nxt, int t, const uint32_t par) {
+      wait_vm_le<0>();
+      __syncthreads();  // K(t+1), V(t) visible; every wave is done with K(t) and V(t-1)
+      if (t + 2 < nst) dma.issue(ks0 + par * TB, kbase, (t + 2) * kStageRows, S - 1, w, lane);
+      dma.issue(vs0 + (par ^ 1) * TB, vbase, (t + 1) * kStageRows, S - 1, w, lane);
+      const uint32_t kso = (par ^ 1) * TB, vso = par * TB;
+      lazy_rescale<DB>(mxc, oacc, m, lsum);
+      const float nm = -m;
+      bf16x8_t kfr[KS], vfr[NPV], pb[2];
+      kfr[0] = kf.rowf(kso, 0);
+      kfr[1] = kf.rowf(kso, 1);
+      nxt = zero16();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < KS; ++i) {
+        if (i + 2 < KS) kfr[i + 2] = kf.rowf(kso, i + 2);
+        else vfr[i + 2 - KS] = vf.trf(vso, (i + 2 - KS) / DB, (i + 2 - KS) % DB);
+        nxt = mfma32(kfr[i], qreg[i], nxt);
+#pragma unroll
+        for (int e = 0; e < EPS; ++e) {
+          const int r = i * EPS + e;
+          cur[r] = __builtin_amdgcn_exp2f(fmaf(cur[r], c, nm));
+          lsum += cur[r];
+        }
+        if (((i + 1) * EPS) % 8 == 0) pb[(i + 1) * EPS / 8 - 1] = pack8(cur, (i + 1) * EPS / 8 - 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      const bf16_t* sK = smem + (t & 1) * 2 * TILE;
-      const bf16_t* sV = sK + TILE;
+#pragma unroll
+      for (int j = 0; j < NPV; ++j) {
+        if (j + 2 < NPV) vfr[j + 2] = vf.trf(vso, (j + 2) / DB, (j + 2) % DB);
+        oacc[j % DB] = mfma32(vfr[j], pb[j / DB], oacc[j % DB]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      mxc = tile_row_max(nxt, c);
+    };
+    int t = 0;
+    for (; t + 1 < nst; ++t) {
+      interior(sa, sb, t, (uint32_t)(t & 1));
+      sa = sb;
+    }
+    // the last stage: masks where a key can lie past the query (diagonal) or past S (tail)
+    wait_vm_le<0>();
+    __syncthreads();
+    {
+      const uint32_t vso = (uint32_t)(t & 1) * TB;
       const int kt0 = t * kStageRows + 32 * ph;
       if (wq0 < S && kt0 < kv_end && !(a.causal && kt0 > wq1)) {
-        floatx16_t st = zero16();
-#pragma unroll
-        for (int i = 0; i < KS; ++i) st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
-        // masks only where a key can lie past the query (diagonal stage) or past S (tail stage)
         if ((a.causal && kt0 + 31 > wq0) || kt0 + 31 >= S) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= S || (a.causal && key > q_row)) st[r] = -INFINITY;
+            if (key >= S || (a.causal && key > q_row)) sa[r] = -INFINITY;
           }
         }
-        // row max on the raw scores (scale > 0), then in scaled log2 units
-        float mx = fmaxf(st[0], st[1]);
-#pragma unroll
-        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, st[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
-        // Lazy rescaling: keep the running max while no row's max grows by more than 8 (so every
-        // p = 2^(s*c - m) stays <= 256, far inside fp32 and bf16 range); the final division by
-        // the row sum makes the result independent of which max was used.
-        if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
-          const float mnew = fmaxf(m, mx);
-          const float corr = __builtin_amdgcn_exp2f(m - mnew);
-          lsum *= corr;
-#pragma unroll
-          for (int d = 0; d < DB; ++d)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
-          m = mnew;
-        }
+        lazy_rescale<DB>(tile_row_max(sa, c), oacc, m, lsum);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[r], c, -m));
-          st[r] = p;
-          lsum += p;
+          sa[r] = __builtin_amdgcn_exp2f(fmaf(sa[r], c, -m));
+          lsum += sa[r];
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8_t pb = pack8(st, s2);
+          const bf16x8_t pb = pack8(sa, s2);
 #pragma unroll
-          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(tr_frag<D>(sV, 32 * ph + 16 * s2, d, fa), pb, oacc[d]);
+          for (int d = 0; d < DB; ++d) oacc[d] = mfma32(vf.trf(vso, s2, d), pb, oacc[d]);
         }
       }
-      wait_vm();
-      __syncthreads();
     }
-    // merge the 4 phases: rescale each phase's partial to the common max, then sum in order
-    float* mbuf = cbuf + 6 * DB * 16 * 64;  // m and lsum of every wave, [phase][sub][lane]
-    mbuf[(ph * 2 + sub) * 64 + lane] = m;
-    mbuf[512 + (ph * 2 + sub) * 64 + lane] = lsum;
+
+    // merge: normaliser of each row over the 4 phases, each wave's share of it
+    __syncthreads();  // every wave is done with the stages, which become the merge buffer
+    mbuf[0][ph][sub][lane] = m;
+    mbuf[1][ph][sub][lane] = lsum;
     __syncthreads();
     float mall = -INFINITY;
 #pragma unroll
-    for (int p = 0; p < kPhases; ++p) mall = fmaxf(mall, mbuf[(p * 2 + sub) * 64 + lane]);
-    const float own = m == -INFINITY ? 0.f : exp2f(m - mall);
+    for (int p = 0; p < kPhases; ++p) mall = fmaxf(mall, mbuf[0][p][sub][lane]);
+    float lall = 0.f;  // whole-row sum (both lane halves hold half of each block's keys)
 #pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[d][r] *= own;
-    float lall = 0.f;
-    if (ph == 0) {
-#pragma unroll
-      for (int p = 0; p < kPhases; ++p) {
-        const float mp = mbuf[(p * 2 + sub) * 64 + lane];
-        const float f = mp == -INFINITY ? 0.f : exp2f(mp - mall);
-        lall += f * mbuf[512 + (p * 2 + sub) * 64 + lane];
-      }
+    for (int p = 0; p < kPhases; ++p) {
+      const float mp = mbuf[0][p][sub][lane];
+      const float f = mp == -INFINITY ? 0.f : exp2f(mp - mall);
+      lall += f * (mbuf[1][p][sub][lane] + mbuf[1][p][sub][lane ^ 32]);
     }
-    merge_phases<0, DB>(cbuf, oacc, w, lane);
-    if (ph == 0) {
-      lall += __shfl_xor(lall, 32, 64);
-      if (q_row < S) {
-        const float inv = 1.f / lall;
-        bf16_t* op = a.o_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
-        if (a.o_lo_out) {
-          bf16_t* olo = a.o_lo_out + (tok0 + q_row) * a.ld_o + (int64_t)h * D;
+    const float share = (m == -INFINITY ? 0.f : exp2f(m - mall)) / lall;
+    // partial outputs as fp32 [phase][row of the item][D], 16-byte chunk j of row q at j ^ (q & 7)
+    float* part = reinterpret_cast<float*>(smem);
+    const int q = 32 * sub + l32;
 #pragma unroll
-          for (int d = 0; d < DB; ++d)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-              st4_split(op + d * 32 + 8 * rr + 4 * g, olo + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
-        } else {
+      for (int rr = 0; rr < 4; ++rr) {
+        floatx4_t v;
 #pragma unroll
-          for (int d = 0; d < DB; ++d)
+        for (int j = 0; j < 4; ++j) v[j] = oacc[db][4 * rr + j] * share;
+        const int chunk = 8 * db + 2 * rr + g;
+        *reinterpret_cast<floatx4_t*>(part + ((ph * 64 + q) * (D / 4) + (chunk ^ (q & 7))) * 4) = v;
+      }
+    if (ph == 0 && g == 0 && q_row < S) a.lse_out[(int64_t)it.bh * S + q_row] = (mall + log2f(lall)) * kLn2;
+    __syncthreads();
+    {
+      constexpr int CPL = D / 32;  // 16-byte fp32 chunks per lane: 8 lanes cover a row
+      const int rq = 8 * w + (lane >> 3), row = it.blk * 64 + rq;
+      floatx4_t acc[CPL];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) st4(op + d * 32 + 8 * rr + 4 * g, oacc[d], rr, inv);
+      for (int j = 0; j < CPL; ++j) acc[j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < kPhases; ++p)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const int chunk = CPL * (lane & 7) + j;
+          acc[j] += *reinterpret_cast<const floatx4_t*>(part + ((p * 64 + rq) * (D / 4) + (chunk ^ (rq & 7))) * 4);
         }
-        if (g == 0) a.lse_out[(int64_t)it.bh * S + q_row] = (mall + log2f(lall)) * kLn2;
+      if (row < S) {
+        const int64_t off = (tok0 + row) * a.ld_o + (int64_t)h * D + 4 * CPL * (lane & 7);
+#pragma unroll
+        for (int j2 = 0; j2 < CPL / 2; ++j2) {
+          u16x8_t hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = acc[2 * j2 + e / 4][e % 4];
+            hi[e] = f32_to_bf16(x);
+            lo[e] = f32_to_bf16(x - bf16_to_f32(hi[e]));
+          }
+          *reinterpret_cast<u16x8_t*>(a.o_out + off + 8 * j2) = hi;
+          if (a.o_lo_out) *reinterpret_cast<u16x8_t*>(a.o_lo_out + off + 8 * j2) = lo;
+        }
       }
     }
+    __syncthreads();  // the merge buffer is read out before the next item's loads overwrite it
   }
 }
 

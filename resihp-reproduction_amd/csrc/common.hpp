@@ -171,6 +171,23 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, const b
       : "memory", "m0");
 }
 
+// dma16s with the LDS destination given as a byte address (wave-uniform): callers that keep their
+// tiles as LDS addresses avoid the generic-to-LDS pointer conversion and its null check.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_dst);
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 4\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sb), "s"(lds)
+      : "memory", "m0");
+}
+
 // wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
 // outstanding; they complete in issue order
 template <int N>
