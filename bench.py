@@ -396,6 +396,46 @@ def xent_leg(dev, reps=5):
             "what": f"{label} at GPT-2-small rows (8x1024 tokens, vocab 50257, bf16), mean of {reps}"}
 
 
+def adamw_leg(dev, reps=10):
+    """One resihp.optim.AdamW step over the fp32 parameters of one TP=4 rank's GPT-1.3B layer (q, k, v
+    512x2048, out 2048x512, fc1 and fc2 2048x2048 shards, two LayerNorms: 10 tensors, 12.6 M values)
+    -- rh_adamw_multi, one launch; 28 bytes per value (param, grad, exp_avg, exp_avg_sq read; param
+    and both moments written).  Cold cache (a 1 GiB buffer written before every step), median."""
+    import torch
+
+    from resihp.optim import AdamW
+
+    d, dl, ff = 2048, 512, 2048
+    shapes = [(dl, d)] * 3 + [(d, dl), (ff, d), (d, ff)] + [(d,)] * 4
+    g = torch.Generator().manual_seed(11)
+    params = []
+    for shp in shapes:
+        t = torch.nn.Parameter((torch.randn(*shp, generator=g) * 0.02).to(dev))
+        t.grad = (torch.randn(*shp, generator=g) * 1e-3).to(dev)
+        params.append(t)
+    opt = AdamW(params, lr=1e-3)
+    opt.step()
+    torch.cuda.synchronize()
+    numel = sum(t.numel() for t in params)
+    moved = 28 * numel
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    evs = []
+    for _ in range(reps):
+        flush.fill_(1)
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
+        opt.step()
+        ev[1].record()
+        evs.append(ev)
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) for a, b in evs)[reps // 2] * 1e3
+    gbps = moved / us / 1e3
+    return {"bytes_per_launch": moved, "mean_us": round(us, 2), "GB/s": round(gbps, 1),
+            "hbm_frac": round(gbps * 1e9 / PEAK_HBM, 4), "launches_per_step": 1,
+            "what": f"AdamW step (rh_adamw_multi, one launch) over one TP4 GPT-1.3B layer's fp32 parameters "
+                    f"({len(params)} tensors, {numel} values); cold cache, median of {reps}"}
+
+
 WORKLOADS = {
     "tp4_shard_gpt1.3b_block": lambda: ShardBlock("tp4_shard_gpt1.3b_block"),
     "gpt2_small_lm": GPT2Small,
@@ -602,6 +642,7 @@ def main(argv=None):
         # the path's other bandwidth kernels, measured in this run at their own workloads' sizes
         hbm["xent_fwd (+ dlogits), GPT-2-small rows"] = xent_leg(dev)
         hbm["reshard_pack, TP4->TP2 d2048/FFN8192 layer"] = reshard_pack_leg(dev)
+        hbm["adamw_multi, one TP4 GPT-1.3B layer (fp32)"] = adamw_leg(dev)
         _log("[bench] extra bandwidth legs done")
 
     cpu = None
