@@ -100,19 +100,55 @@ __global__ __launch_bounds__(64) void adamw_step_increment(AdamMultiArgs<float> 
   }
 }
 
+// One AdamW update in fp32 of values read from T storage; returns the new param and moments as
+// they are stored (the update divides by the stored, i.e. rounded, moments, as torch does).
+template <typename T>
+__device__ __forceinline__ void adamw_math(float& w, float gr, float& mv, float& vv, float decay, float omb1, float b2f,
+                                           float omb2, float step_size, float bc2_sqrt, float eps) {
+  w *= decay;
+  mv = Storage<T>::to_f32(Storage<T>::from_f32(mv + (gr - mv) * omb1));
+  vv = Storage<T>::to_f32(Storage<T>::from_f32(vv * b2f + omb2 * gr * gr));
+  w = w - step_size * (mv / (sqrtf(vv) / bc2_sqrt + eps));
+}
+
 template <typename T>
 __device__ __forceinline__ void adamw_update(T* p, const T* g, T* m, T* v, float decay, float omb1, float b2f,
                                              float omb2, float step_size, float bc2_sqrt, float eps) {
-  float w = ld_f32(p) * decay;
-  const float gr = ld_f32(g);
-  float mv = ld_f32(m);
-  mv = mv + (gr - mv) * omb1;
-  const float vv = ld_f32(v) * b2f + omb2 * gr * gr;
+  float w = ld_f32(p), mv = ld_f32(m), vv = ld_f32(v);
+  adamw_math<T>(w, ld_f32(g), mv, vv, decay, omb1, b2f, omb2, step_size, bc2_sqrt, eps);
   st_f32(m, mv);
   st_f32(v, vv);
-  const float mq = ld_f32(m), vq = ld_f32(v);  // the stored (rounded) moments, as torch uses them
-  w = w - step_size * (mq / (sqrtf(vq) / bc2_sqrt + eps));
   st_f32(p, w);
+}
+
+// Four consecutive elements per thread with one 16-byte (fp32) or 8-byte (bf16) access per array.
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct Vec4<bf16_t> {
+  typedef uint16_t type __attribute__((ext_vector_type(4)));
+};
+template <typename T>
+__device__ __forceinline__ void adamw_update4(T* p, const T* g, T* m, T* v, float decay, float omb1, float b2f,
+                                              float omb2, float step_size, float bc2_sqrt, float eps) {
+  using V = typename Vec4<T>::type;
+  V pv = *reinterpret_cast<const V*>(p), gv = *reinterpret_cast<const V*>(g);
+  V mv4 = *reinterpret_cast<const V*>(m), vv4 = *reinterpret_cast<const V*>(v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float w = Storage<T>::to_f32(pv[j]), mv = Storage<T>::to_f32(mv4[j]), vv = Storage<T>::to_f32(vv4[j]);
+    adamw_math<T>(w, Storage<T>::to_f32(gv[j]), mv, vv, decay, omb1, b2f, omb2, step_size, bc2_sqrt, eps);
+    pv[j] = Storage<T>::from_f32(w);
+    mv4[j] = Storage<T>::from_f32(mv);
+    vv4[j] = Storage<T>::from_f32(vv);
+  }
+  *reinterpret_cast<V*>(m) = mv4;
+  *reinterpret_cast<V*>(v) = vv4;
+  *reinterpret_cast<V*>(p) = pv;
 }
 
 template <typename T>
@@ -132,7 +168,14 @@ __global__ __launch_bounds__(kThreads) void adamw_multi_kernel(AdamMultiArgs<T> 
   const T* g = a.g[t];
   T* m = a.m[t];
   T* v = a.v[t];
-  for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads)
+  const uintptr_t al = (uintptr_t)p | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v;
+  int64_t i = lo;
+  if (al % (4 * sizeof(T)) == 0) {  // chunk starts are multiples of 4 elements
+    for (i = lo + 4 * (int64_t)threadIdx.x; i + 3 < hi; i += 4 * kThreads)
+      adamw_update4(p + i, g + i, m + i, v + i, decay, omb1, b2f, omb2, step_size, bc2_sqrt, eps);
+    i = lo + (hi - lo) / 4 * 4;  // the last < 4 elements of the chunk
+  }
+  for (i += threadIdx.x; i < hi; i += kThreads)
     adamw_update(p + i, g + i, m + i, v + i, decay, omb1, b2f, omb2, step_size, bc2_sqrt, eps);
 }
 
