@@ -147,6 +147,10 @@ int rh_gemm_grouped_workspace_bytes(const rh_gemm_desc* descs, int n, int64_t* b
 int rh_gemm_grouped(const rh_gemm_desc* descs, int n, void* workspace, int64_t workspace_bytes,
                     void* stream);
 int rh_gemm_grouped_plan(const rh_gemm_desc* descs, int n, int* splits);
+/* The kernel the single launch would run (its template name, as profilers print it), or "none"
+ * when the group runs as consecutive rh_gemm calls.  No counterpart in the reference
+ * (profiling support). */
+int rh_gemm_grouped_kernel_name(const rh_gemm_desc* descs, int n, char* buf, int64_t len);
 
 /* ---- causal self-attention core ---------------------------------------------
  * Replaces  scores = q @ k^T / sqrt(Dh); masked_fill(triu(ones,1), -inf);

@@ -149,6 +149,17 @@ __device__ __forceinline__ void dma16(const bf16_t* src, const bf16_t* lds_dst) 
       : "memory", "m0");
 }
 
+// The same with the LDS destination given as a wave-uniform 32-bit LDS byte address.
+__device__ __forceinline__ void dma16(const bf16_t* src, uint32_t lds_dst) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_dst))
+      : "memory", "m0");
+}
+
 // The same load in saddr form: lane l fetches the 16 bytes at sbase + voff (sbase wave-uniform,
 // held in SGPRs; voff a 32-bit per-lane byte offset), so a stage of loads needs one 32-bit
 // offset register per load instead of a 64-bit pointer.

@@ -97,8 +97,10 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
     return RH_OK;
   }
   const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
-  snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma_ok(desc, pl, p) ? "gemm_bf16_dma" : "gemm_bf16_mfma",
-           kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, kWaves[pl.cfg][0], kWaves[pl.cfg][1], desc->layout,
+  const bool dma = dma_ok(desc, pl, p);
+  const bool w4 = dma && pl.cfg == kT256x256 && four_wave_256(false);  // as launch_cfg decides
+  snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma ? "gemm_bf16_dma" : "gemm_bf16_mfma",
+           kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, kWaves[pl.cfg][0], w4 ? 2 : kWaves[pl.cfg][1], desc->layout,
            pl.splits + pl.tail > 1 ? 0 : desc->epilogue,  // split slices use the RH_EPI_NONE kernels
            split);
   return RH_OK;
@@ -185,6 +187,24 @@ extern "C" int rh_gemm_grouped(const rh_gemm_desc* descs, int n, void* workspace
     case RH_GEMM_NN: return launch_grouped<RH_GEMM_NN>(descs, n, g, workspace, st);
     default: return launch_grouped<RH_GEMM_TN>(descs, n, g, workspace, st);
   }
+}
+
+extern "C" int rh_gemm_grouped_kernel_name(const rh_gemm_desc* descs, int n, char* buf, int64_t len) {
+  RH_REQUIRE(buf != nullptr && len > 0, "rh_gemm_grouped_kernel_name: null or empty buffer");
+  RH_REQUIRE(n >= 0 && (n == 0 || descs), "rh_gemm_grouped_kernel_name: bad descriptor list");
+  for (int i = 0; i < n; ++i) {
+    int rc = validate(&descs[i]);
+    if (rc) return rc;
+  }
+  const GroupPlan g = plan_grouped(descs, n);
+  if (!g.ok) {
+    snprintf(buf, (size_t)len, "none");
+    return RH_OK;
+  }
+  const bool w4 = four_wave_256(true);
+  snprintf(buf, (size_t)len, "gemm_bf16_dma_grouped<256, 256, 2, %d, %d, %s>", w4 ? 2 : 4, descs[0].layout,
+           g.splits > 1 ? "true" : "false");
+  return RH_OK;
 }
 
 extern "C" int rh_gemm_grouped_plan(const rh_gemm_desc* descs, int n, int* splits) {

@@ -343,6 +343,35 @@ __device__ __forceinline__ void mma_ktile(const bf16_t* a_s, const bf16_t* b_s, 
   }
 }
 
+// Accumulate into AGPRs.  A 128x128 wave tile needs 256 accumulator registers, all of the
+// architectural VGPRs, so they must live in the accumulation registers; with the builtin the
+// register allocator keeps them in VGPRs and spills.  The compiler does not see this as an MFMA:
+// the caller waits out the MFMA-result hazard (mfma_asm_drain) before reading the accumulators.
+__device__ __forceinline__ void mfma_agpr(floatx16_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Volatile asm statements keep their order, so an empty statement that "modifies" every
+// accumulator after the wait pins every later read of them behind it.
+template <int FM, int FN>
+__device__ __forceinline__ void agpr_fence(floatx16_t (&acc)[FM][FN]) {
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));
+}
+// Before the first MFMA: the accumulators' zeroing (VALU writes) is done, plus 5 wait states.
+template <int FM, int FN>
+__device__ __forceinline__ void mfma_asm_begin(floatx16_t (&acc)[FM][FN]) {
+  agpr_fence(acc);
+  asm volatile("s_nop 4" ::: "memory");
+}
+// After the last MFMA: 24 wait states, more than a 32x32x16 MFMA's result latency for a VALU read.
+template <int FM, int FN>
+__device__ __forceinline__ void mfma_asm_drain(floatx16_t (&acc)[FM][FN]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  agpr_fence(acc);
+}
+
 // 4x4 transpose across the four lanes of each quad (DPP quad_perm, two exchange stages): on
 // entry lane s = lane % 4 holds v[t] = element (t, s) of a 4x4 block, on exit element (s, t).
 template <int CTRL>
@@ -379,16 +408,18 @@ __device__ __forceinline__ void epilogue_regs(const GemmParams<bf16_t>& p, float
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const floatx16_t a = acc[i][j];  // a register copy: the rolled loop below indexes it by r
+#pragma unroll 1
         for (int r = 0; r < 16; ++r) {
           const int64_t m = wr0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), n = wc0 + j * 32 + (lane & 31);
           if (m >= p.M || n >= p.N) continue;
           if (SPLIT)
-            p.ws[(int64_t)split * p.M * p.N + m * p.N + n] = acc[i][j][r];
+            p.ws[(int64_t)split * p.M * p.N + m * p.N + n] = a[r];
           else
-            epilogue_store<bf16_t, EPI>(p, m, n, acc[i][j][r]);
+            epilogue_store<bf16_t, EPI>(p, m, n, a[r]);
         }
+      }
     return;
   }
   // after the transpose: row wr0 + i*32 + 8*q + 4*g + lane%4, columns wc0 + j*32 + (lane & 28) + 0..3
@@ -841,17 +872,187 @@ struct DmaOperand {
   }
   __device__ __forceinline__ void issue(bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int win = wave + NWAVES * i;
-      dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + win * 512);
-    }
+    for (int i = 0; i < PER; ++i) issue_one(i, dst, kt, krow0, wave);
+  }
+  __device__ __forceinline__ void issue_one(int i, bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
+    const int win = wave + NWAVES * i;
+    dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + win * 512);
+  }
+  // the same with the LDS destination as a 32-bit LDS byte address (wave-uniform, scalar math)
+  __device__ __forceinline__ void issue_one(int i, uint32_t dst, int kt, const bf16_t* krow0, int wave) {
+    const int win = wave + NWAVES * i;
+    dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + (uint32_t)win * 1024u);
   }
 };
+
+// 256x256 tile on 4 waves (2 x 2, 128x128 per wave): a third fewer LDS fragment reads per MFMA
+// than 8 waves of 128x64, and one wave per SIMD, so no two waves contend for one MFMA pipe.  The
+// 256 accumulators per lane live in AGPRs (mfma_agpr).  One wave per SIMD cannot hide a stall
+// behind another wave, so the k-tile is software-pipelined by hand; volatile asm statements keep
+// their order and the LDS reads / DMA issues written between them stay where they are written:
+//   k-steps 0..2: 16 MFMAs each, the next k-step's 8 fragments read one after each of the first
+//     8 MFMAs (16 for transposing reads);
+//   then wait for this wave's loads of tile kt+1 and the barrier (tile kt+1 visible everywhere,
+//     every wave's reads of tile kt done: __syncthreads waits for them);
+//   k-step 3: 16 MFMAs on fragments already in registers, with tile kt+1's k-step-0 fragments
+//     read and tile kt+2's 16 DMA windows issued (into tile kt's stage) between them.
+// So the only pipe bubble per k-tile is the barrier itself, which the waves reach together.
+template <int BM, int BN, int L, int EPI, bool SPLIT>
+__device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf16_t* smem, int tm, int tn, int split) {
+  constexpr int WGM = 2, WGN = 2, NW = 4;
+  constexpr bool A_KC = (L != RH_GEMM_TN);
+  constexpr bool B_KC = (L == RH_GEMM_NT);
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK, STAGE = A_ELEMS + B_ELEMS;
+  using DA = DmaOperand<BM, A_KC, NW>;
+  using DB = DmaOperand<BN, B_KC, NW>;
+  static_assert(FM == 4 && FN == 4 && DA::PER + DB::PER == 16, "4-wave 256x256 tile");
+
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
+  const int64_t kend = min(p.K, kbeg + p.k_per_split);
+  const int nk = (int)((kend - kbeg) / kBK);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  DA da;
+  DB db;
+  da.setup([&](int64_t r) { return p.A + r * p.lda; }, m0, p.M, kbeg, p.lda, wave, lane);
+  db.setup([&](int64_t r) { return b_row(p, r); }, n0, p.N, kbeg, p.ldb, wave, lane);
+  const bf16_t* const bs0 = p.B[0];
+  const bf16_t* const bs1 = p.B[1 % RH_MAX_SEG];
+  const bf16_t* const bs2 = p.B[2 % RH_MAX_SEG];
+  const bf16_t* const bs3 = p.B[3 % RH_MAX_SEG];
+  const int bseg_rows = (!B_KC && p.b_nseg > 1) ? (int)p.b_seg : INT32_MAX;
+  int iss_seg = 0, iss_row = (int)kbeg;
+  if (!B_KC && p.b_nseg > 1) {
+    iss_seg = (int)kbeg / bseg_rows;
+    iss_row = (int)kbeg - iss_seg * bseg_rows;
+  }
+  // first k-row of the next m/n-contiguous B k-tile to issue (tiles are issued in order)
+  auto next_b = [&]() -> const bf16_t* {
+    if (B_KC) return nullptr;
+    const bf16_t* base = iss_seg == 0 ? bs0 : iss_seg == 1 ? bs1 : iss_seg == 2 ? bs2 : bs3;
+    const bf16_t* r = base + (int64_t)iss_row * p.ldb;
+    iss_row += kBK;
+    if (iss_row >= bseg_rows) {
+      iss_row -= bseg_rows;
+      ++iss_seg;
+    }
+    return r;
+  };
+  auto a_krow = [&](int kt) -> const bf16_t* { return A_KC ? nullptr : p.A + (kbeg + (int64_t)kt * kBK) * p.lda; };
+  // LDS: A in three stages (tile t in stage t % 3), B in two (t % 2), 160 KB in all.  The A stage
+  // of tile kt+2 is free from tile kt-1's barrier on, so its loads spread over k-steps 0..2 of
+  // tile kt; only B's wait for tile kt's own barrier.  (The DMA path moves about 64 B per clock
+  // per CU, so a whole k-tile's 64 windows per CU take about half of the k-tile's MFMA time.)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;  // a generic LDS pointer's low 32 bits
+  constexpr uint32_t kABytes = A_ELEMS * 2, kBBytes = B_ELEMS * 2;
+  auto a_lds = [&](int stage) { return lds0 + (uint32_t)stage * kABytes; };
+  auto b_lds = [&](int stage) { return lds0 + 3u * kABytes + (uint32_t)stage * kBBytes; };
+  auto a_ptr = [&](int stage) -> const bf16_t* { return smem + stage * A_ELEMS; };
+  auto b_ptr = [&](int stage) -> const bf16_t* { return smem + 3 * A_ELEMS + stage * B_ELEMS; };
+  auto issue_all = [&](int kt) {
+    const bf16_t* ak = a_krow(kt);
+    const bf16_t* bk = next_b();
+#pragma unroll
+    for (int i = 0; i < DA::PER; ++i) da.issue_one(i, a_lds(kt % 3), kt, ak, wave);
+#pragma unroll
+    for (int i = 0; i < DB::PER; ++i) db.issue_one(i, b_lds(kt & 1), kt, bk, wave);
+  };
+
+  floatx16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  mfma_asm_begin(acc);
+
+  bf16x8_t fa[2][FM], fb[2][FN];
+  auto frag = [&](int set, const bf16_t* sa, const bf16_t* sb, int ks, int f) {
+    if (f < FM) fa[set][f] = load_frag<BM, A_KC>(sa, wm * WTM + f * 32, ks, lane);
+    else fb[set][f - FM] = load_frag<BN, B_KC>(sb, wn * WTN + (f - FM) * 32, ks, lane);
+  };
+
+  if (nk > 0) {
+    issue_all(0);
+    if (nk > 1) {
+      issue_all(1);
+      wait_vm_le<DA::PER + DB::PER>();  // tile 0 has landed, tile 1 may be in flight
+    } else {
+      wait_vm_le<0>();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < FM + FN; ++f) frag(0, a_ptr(0), b_ptr(0), 0, f);
+  }
+  // one k-tile; MORE: a next tile exists (read its first fragments), REFILL: tile kt+2 exists.
+  // sa3 = kt % 3 is carried by the caller (no division in the loop).
+  static_assert(DA::PER == 8 && DB::PER == 8, "eight windows per wave and operand");
+  auto ktile = [&](int kt, int sa3, auto more_c, auto refill_c) {
+    constexpr bool MORE = decltype(more_c)::value, REFILL = decltype(refill_c)::value;
+    const int na3 = sa3 == 2 ? 0 : sa3 + 1, fa3 = na3 == 2 ? 0 : na3 + 1;  // stages of kt+1, kt+2
+    const bf16_t* sa = a_ptr(sa3);
+    const bf16_t* sb = b_ptr(kt & 1);
+    const bf16_t* ak = nullptr;
+    if constexpr (REFILL) ak = a_krow(kt + 2);
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks) {
+#pragma unroll
+      for (int t = 0; t < FM * FN; ++t) {
+        mfma_agpr(acc[t / FN][t % FN], fa[ks & 1][t / FN], fb[ks & 1][t % FN]);
+        if (t < FM + FN) frag((ks + 1) & 1, sa, sb, ks + 1, t);
+        if constexpr (REFILL) {
+          const int g = ks * 16 + t;  // A windows of tile kt+2 at MFMA slots 3, 9, ..., 45
+          if (g % 6 == 3) da.issue_one(g / 6, a_lds(fa3), kt + 2, ak, wave);
+        }
+      }
+    }
+    // this wave's loads of tile kt+1 have landed (the 8 A windows of tile kt+2 may be in flight)
+    if constexpr (REFILL) wait_vm_le<DA::PER>();
+    else wait_vm_le<0>();
+    __syncthreads();
+    const bf16_t* bk = nullptr;
+    if constexpr (REFILL) bk = next_b();
+#pragma unroll
+    for (int t = 0; t < FM * FN; ++t) {
+      mfma_agpr(acc[t / FN][t % FN], fa[1][t / FN], fb[1][t % FN]);
+      if constexpr (MORE) {
+        if (t < FM + FN) frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, t);
+      }
+      if constexpr (REFILL) {
+        if (t % 2 == 0) db.issue_one(t / 2, b_lds(kt & 1), kt + 2, bk, wave);
+      }
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  int kt = 0, s3 = 0;
+#pragma unroll 1
+  for (; kt + 2 < nk; ++kt) {
+    ktile(kt, s3, T_{}, T_{});
+    s3 = s3 == 2 ? 0 : s3 + 1;
+  }
+  if (kt + 1 < nk) {
+    ktile(kt++, s3, T_{}, F_{});
+    s3 = s3 == 2 ? 0 : s3 + 1;
+  }
+  if (kt < nk) ktile(kt, s3, F_{}, F_{});
+  mfma_asm_drain(acc);
+  // the register epilogue: staging the tile through LDS makes the allocator spill accumulators
+  epilogue_regs<BM, BN, WGM, WGN, EPI, SPLIT>(p, acc, m0, n0, wm, wn, lane, split);
+}
 
 // One output tile (tm, tn) of split `split` of a direct-to-LDS GEMM, on the workgroup's LDS `smem`
 // (two stages of BM x 64 + BN x 64 bf16).
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
 __device__ __forceinline__ void gemm_dma_tile(const GemmParams<bf16_t>& p, bf16_t* smem, int tm, int tn, int split) {
+  if constexpr (WGM * WGN == 4 && BM == 256 && BN == 256) {
+    gemm_dma_tile_w4<BM, BN, L, EPI, SPLIT>(p, smem, tm, tn, split);
+    return;
+  }
   constexpr int NW = WGM * WGN;
   constexpr bool A_KC = (L != RH_GEMM_TN);
   constexpr bool B_KC = (L == RH_GEMM_NT);
@@ -946,9 +1147,15 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmParams<bf16_t>& p, bf16_
   epilogue_sel<BM, BN, WGM, WGN, EPI, SPLIT, 2 * STAGE>(p, smem, acc, m0, n0, wm, wn, lane, split);
 }
 
+// LDS of a direct-to-LDS tile: two stages of A and B; the 4-wave 256x256 tile keeps three of A
+template <int BM, int BN, int WGM, int WGN>
+constexpr int dma_smem_elems() {
+  return (WGM * WGN == 4 && BM == 256 && BN == 256) ? (3 * BM + 2 * BN) * kBK : 2 * (BM + BN) * kBK;
+}
+
 template <int BM, int BN, int WGM, int WGN, int L, int EPI, bool SPLIT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma(GemmParams<bf16_t> p) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (BM + BN) * kBK];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[dma_smem_elems<BM, BN, WGM, WGN>()];
   int tm, tn;
   tile_coords(p.tiles_m, p.tiles_n, p.group_m, tm, tn);
   gemm_dma_tile<BM, BN, WGM, WGN, L, EPI, SPLIT>(p, smem, tm, tn, (int)blockIdx.z);
@@ -982,7 +1189,7 @@ __device__ __forceinline__ void group_order(int t, int tiles_m, int tiles_n, int
 
 template <int BM, int BN, int WGM, int WGN, int L, bool SPLIT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_dma_grouped(GroupedParams gp) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (BM + BN) * kBK];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[dma_smem_elems<BM, BN, WGM, WGN>()];
   const int nwg = gp.first[gp.count];
   const int bid = blockIdx.x;
   const int q = nwg / 8, r = nwg % 8;
@@ -1311,10 +1518,24 @@ void launch_bf16(const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t s
   else hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
 }
 
+// Which kernel runs a 256x256 direct-to-LDS tile: the 4-wave one (gemm_dma_tile_w4) for grouped
+// launches (the weight gradients: long K, no epilogue), the 8-wave one for single GEMMs, whose
+// epilogues (GELU, residual) it finishes faster through LDS (measured inside the block's step).
+// RESIHP_GEMM_WAVES=4 or 8 pins one for both (tests run both).
+inline bool four_wave_256(bool grouped) {
+  const char* e = getenv("RESIHP_GEMM_WAVES");
+  if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] == '4';
+  return grouped;
+}
+
 template <int L, int EPI, bool SPLIT>
 void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t st) {
   switch (cfg) {
-    case kT256x256: launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st); break;
+    case kT256x256:
+      if (dma && four_wave_256(false))
+        hipLaunchKernelGGL((gemm_bf16_dma<256, 256, 2, 2, L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
+      else launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st);
+      break;
     case kT256x128: launch_bf16<256, 128, 4, 2, L, EPI, SPLIT>(p, dma, grid, st); break;
     case kT256x192:
       if constexpr (L == RH_GEMM_NT) launch_bf16<256, 192, 4, 2, L, EPI, SPLIT>(p, dma, grid, st);
@@ -1482,7 +1703,12 @@ int launch_grouped(const rh_gemm_desc* d, int n, const GroupPlan& g, void* ws, h
   gp.first[n] = total;
   gp.count = n;
   gp.splits = g.splits;
-  if (g.splits > 1)
+  if (four_wave_256(true)) {
+    if (g.splits > 1)
+      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, true>), dim3((unsigned)total), dim3(256), 0, st, gp);
+    else
+      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, false>), dim3((unsigned)total), dim3(256), 0, st, gp);
+  } else if (g.splits > 1)
     hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, true>), dim3((unsigned)total), dim3(512), 0, st, gp);
   else
     hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, false>), dim3((unsigned)total), dim3(512), 0, st, gp);

@@ -106,6 +106,7 @@ _SIGNATURES = {
     "rh_gemm_grouped_workspace_bytes": [ctypes.POINTER(rh_gemm_desc), c_int, ctypes.POINTER(c_i64)],
     "rh_gemm_grouped": [ctypes.POINTER(rh_gemm_desc), c_int, c_ptr, c_i64, c_ptr],
     "rh_gemm_grouped_plan": [ctypes.POINTER(rh_gemm_desc), c_int, ctypes.POINTER(c_int)],
+    "rh_gemm_grouped_kernel_name": [ctypes.POINTER(rh_gemm_desc), c_int, ctypes.c_char_p, c_i64],
     "rh_attn_fwd": [c_int, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr,
                     c_float, c_int, c_ptr],
     "rh_attn_bwd_workspace_bytes": [c_i64, c_i64, c_i64, ctypes.POINTER(c_i64)],

@@ -252,9 +252,11 @@ def linear_wgrad_group(items: list) -> None:
     if profiling.active():
         splits = ctypes.c_int(0)
         H.call("rh_gemm_grouped_plan", descs, len(setups), ctypes.byref(splits))
+        name = ctypes.create_string_buffer(128)
+        H.call("rh_gemm_grouped_kernel_name", descs, len(setups), name, 128)
         flops = sum(2.0 * s[0].M * s[0].N * s[0].K for s in setups)
-        label = (f"gemm_bf16_dma_grouped<256, 256, 2, 4, 2, {'true' if splits.value > 1 else 'false'}>"
-                 + (" + split-K reduce" if splits.value > 1 else "")) if splits.value else "gemm (group as single calls)"
+        label = (name.value.decode() + (" + split-K reduce" if splits.value > 1 else "")) if splits.value \
+            else "gemm (group as single calls)"
         with profiling.launch(label, flops):
             H.call("rh_gemm_grouped", descs, len(setups), H.ptr(ws), nbytes, stream)
     else:

@@ -42,12 +42,17 @@ SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8,
           (256, 384, 1000)]  # ragged K with aligned M/N: direct-to-LDS bulk + register-staged K tail
 
 
-@pytest.fixture(params=["auto", "0", "1", "2", "3"])
+@pytest.fixture(params=["auto", "0", "0w4", "1", "2", "3"])
 def gemm_tile(request, monkeypatch):
     """Pin the bf16 GEMM tile shape (256x256 / 256x128 / 128x128 / 256x192, the last for NT
-    only) or let the planner choose."""
+    only) or let the planner choose; "0w4" is 256x256 on the 4-wave kernel instead of the 8-wave
+    one."""
+    monkeypatch.delenv("RESIHP_GEMM_WAVES", raising=False)
     if request.param == "auto":
         monkeypatch.delenv("RESIHP_GEMM_TILE", raising=False)
+    elif request.param == "0w4":
+        monkeypatch.setenv("RESIHP_GEMM_TILE", "0")
+        monkeypatch.setenv("RESIHP_GEMM_WAVES", "4")
     else:
         monkeypatch.setenv("RESIHP_GEMM_TILE", request.param)
     return request.param
@@ -552,11 +557,13 @@ def _wgrad_desc(dy, x, D, beta, d_seg=0):
     ([(768, 3072), (3072, 768), (768, 768), (2304, 768)], 2),
     ([(256, 512)], None),
 ])
-def test_gemm_grouped_weight_gradients(cuda, shapes, want_splits):
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_gemm_grouped_weight_gradients(cuda, shapes, want_splits, waves, monkeypatch):
     """rh_gemm_grouped over a block's weight gradients (dW = dy^T x, K = tokens): every problem
     equals its fp32 product within bf16 rounding, accumulates into existing gradients (beta 1), writes
     three q|k|v row segments, and agrees with separate rh_gemm calls; the plan uses the expected
-    split count."""
+    split count.  Both 256x256 kernels (4 and 8 waves) are run."""
+    monkeypatch.setenv("RESIHP_GEMM_WAVES", waves)
     T = 8192
     descs, outs, refs, keep = [], [], [], []
     for i, (m, n) in enumerate(shapes):
