@@ -988,6 +988,12 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
 #pragma unroll
     for (int f = 0; f < FM + FN; ++f) frag(0, a_ptr(0), b_ptr(0), 0, f);
   }
+#ifndef RH_W4_SPREAD
+#define RH_W4_SPREAD 1
+#endif
+  // Fragment reads, one every other MFMA, in the order the next k-step's MFMAs (row-major over
+  // the 4 x 4 accumulator blocks) first need them: A0, B0..B3, A1, A2, A3.
+  auto frag_order = [](int slot) { return slot == 0 ? 0 : slot < 5 ? FM + slot - 1 : slot - 4; };
   // one k-tile; MORE: a next tile exists (read its first fragments), REFILL: tile kt+2 exists.
   // sa3 = kt % 3 is carried by the caller (no division in the loop).
   static_assert(DA::PER == 8 && DB::PER == 8, "eight windows per wave and operand");
@@ -1003,7 +1009,7 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
 #pragma unroll
       for (int t = 0; t < FM * FN; ++t) {
         mfma_agpr(acc[t / FN][t % FN], fa[ks & 1][t / FN], fb[ks & 1][t % FN]);
-        if (t < FM + FN) frag((ks + 1) & 1, sa, sb, ks + 1, t);
+        if (RH_W4_SPREAD ? (t % 2 == 0) : (t < FM + FN)) frag((ks + 1) & 1, sa, sb, ks + 1, frag_order(RH_W4_SPREAD ? t / 2 : t));
         if constexpr (REFILL) {
           const int g = ks * 16 + t;  // A windows of tile kt+2 at MFMA slots 3, 9, ..., 45
           if (g % 6 == 3) da.issue_one(g / 6, a_lds(fa3), kt + 2, ak, wave);
@@ -1020,10 +1026,11 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
     for (int t = 0; t < FM * FN; ++t) {
       mfma_agpr(acc[t / FN][t % FN], fa[1][t / FN], fb[1][t % FN]);
       if constexpr (MORE) {
-        if (t < FM + FN) frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, t);
+        if (RH_W4_SPREAD ? (t % 2 == 0) : (t < FM + FN))
+          frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, frag_order(RH_W4_SPREAD ? t / 2 : t));
       }
       if constexpr (REFILL) {
-        if (t % 2 == 0) db.issue_one(t / 2, b_lds(kt & 1), kt + 2, bk, wave);
+        if (t % 2 == RH_W4_SPREAD) db.issue_one(t / 2, b_lds(kt & 1), kt + 2, bk, wave);
       }
     }
   };
