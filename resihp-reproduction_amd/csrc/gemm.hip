@@ -98,7 +98,7 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
   }
   const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
   const bool dma = dma_ok(desc, pl, p);
-  const bool w4 = dma && pl.cfg == kT256x256 && four_wave_256(false);  // as launch_cfg decides
+  const bool w4 = dma && pl.cfg == kT256x256 && four_wave_256(false) && p.w4;  // as launch_cfg decides
   snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma ? "gemm_bf16_dma" : "gemm_bf16_mfma",
            kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, kWaves[pl.cfg][0], w4 ? 2 : kWaves[pl.cfg][1], desc->layout,
            pl.splits + pl.tail > 1 ? 0 : desc->epilogue,  // split slices use the RH_EPI_NONE kernels
@@ -201,7 +201,8 @@ extern "C" int rh_gemm_grouped_kernel_name(const rh_gemm_desc* descs, int n, cha
     snprintf(buf, (size_t)len, "none");
     return RH_OK;
   }
-  const bool w4 = four_wave_256(true);
+  bool w4 = four_wave_256(true);
+  for (int i = 0; i < n; ++i) w4 = w4 && w4_addressable(&descs[i]);  // as launch_grouped decides
   snprintf(buf, (size_t)len, "gemm_bf16_dma_grouped<256, 256, 2, %d, %d, %s>", w4 ? 2 : 4, descs[0].layout,
            g.splits > 1 ? "true" : "false");
   return RH_OK;

@@ -83,6 +83,7 @@ struct GemmParams {
   int aligned;          // all rows 16-byte aligned -> vector loads
   int out_vec;          // D/C/aux rows 8-byte aligned, split partials 16-byte aligned
   int epi_lds;          // finish through LDS (epilogue_tile_impl) instead of epilogue_regs
+  int w4;               // the 4-wave 256x256 kernel may address the operands (w4_addressable)
   int tiles_m, tiles_n, group_m;
   // next-token cross-entropy epilogues of the LM head (kEpiLsePartial, kEpiXentGrad); row m of the
   // output is token m = b*seq + s, scored against tokens[m + 1] unless s == seq - 1, and output
@@ -885,6 +886,43 @@ struct DmaOperand {
   }
 };
 
+// DmaOperand with 32-bit per-lane byte offsets from a wave-uniform base (the saddr form of the
+// load): half the VGPRs of 64-bit pointers.  KC: the base is the operand's first row at the
+// k-tile (one allocation: rows r < extent at base + r*ld); !KC: the k-tile's first row.  The host
+// keeps the offsets below 2^32 bytes (w4_addressable).
+template <int ROWS, bool KC, int NWAVES>
+struct DmaOperand32 {
+  static constexpr int WIN = ROWS * kBK * 2 / 1024;
+  static constexpr int PER = WIN / NWAVES;
+  static_assert(WIN % NWAVES == 0, "tile windows must split evenly over the waves");
+  static constexpr int KROWS = 512 / ROWS;  // !KC: k-rows per window
+  uint32_t voff[PER];
+
+  __device__ __forceinline__ void setup(int64_t o0, int64_t extent, int64_t kbeg, int64_t ld, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int win = wave + NWAVES * i;
+      if (KC) {
+        const int row = win * 8 + lane / 8;
+        const int lchunk = (lane & 7) ^ ((row >> 1) & 7);  // inverse of kc_off's chunk swizzle
+        const int64_t gr = min(o0 + row, extent - 1);
+        voff[i] = (uint32_t)((gr * ld + kbeg + lchunk * 8) * 2);
+      } else {
+        const int kr = win * KROWS + lane / (ROWS / 8);
+        const int pchunk = lane % (ROWS / 8);
+        const int lunit = (pchunk >> 2) ^ (kr & 3);  // inverse of mc_off's unit swizzle
+        const int64_t c = o0 + lunit * 32 + (pchunk & 3) * 8;
+        voff[i] = (uint32_t)(((int64_t)kr * ld + min(c, extent - 8)) * 2);
+      }
+    }
+  }
+  // window i of the k-tile whose base is `base` (KC: operand base + kt*64; !KC: the k-tile's first row)
+  __device__ __forceinline__ void issue_one(int i, uint32_t dst, const bf16_t* base, int wave) {
+    const int win = wave + NWAVES * i;
+    dma16s(base, voff[i], dst + (uint32_t)win * 1024u);
+  }
+};
+
 // 256x256 tile on 4 waves (2 x 2, 128x128 per wave): a third fewer LDS fragment reads per MFMA
 // than 8 waves of 128x64, and one wave per SIMD, so no two waves contend for one MFMA pipe.  The
 // 256 accumulators per lane live in AGPRs (mfma_agpr).  One wave per SIMD cannot hide a stall
@@ -904,8 +942,9 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
   constexpr bool B_KC = (L == RH_GEMM_NT);
   constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
   constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK, STAGE = A_ELEMS + B_ELEMS;
-  using DA = DmaOperand<BM, A_KC, NW>;
-  using DB = DmaOperand<BN, B_KC, NW>;
+  using DA = DmaOperand32<BM, A_KC, NW>;  // A: one allocation
+  using DB = DmaOperand<BN, B_KC, NW>;    // B: k-contiguous rows may come from several segments
+  using DB32 = DmaOperand32<BN, B_KC, NW>;
   static_assert(FM == 4 && FN == 4 && DA::PER + DB::PER == 16, "4-wave 256x256 tile");
 
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -916,9 +955,10 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
   const int wm = wave / WGN, wn = wave % WGN;
 
   DA da;
-  DB db;
-  da.setup([&](int64_t r) { return p.A + r * p.lda; }, m0, p.M, kbeg, p.lda, wave, lane);
-  db.setup([&](int64_t r) { return b_row(p, r); }, n0, p.N, kbeg, p.ldb, wave, lane);
+  std::conditional_t<B_KC, DB, DB32> db;
+  da.setup(m0, p.M, kbeg, p.lda, wave, lane);
+  if constexpr (B_KC) db.setup([&](int64_t r) { return b_row(p, r); }, n0, p.N, kbeg, p.ldb, wave, lane);
+  else db.setup(n0, p.N, kbeg, p.ldb, wave, lane);
   const bf16_t* const bs0 = p.B[0];
   const bf16_t* const bs1 = p.B[1 % RH_MAX_SEG];
   const bf16_t* const bs2 = p.B[2 % RH_MAX_SEG];
@@ -941,7 +981,14 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
     }
     return r;
   };
-  auto a_krow = [&](int kt) -> const bf16_t* { return A_KC ? nullptr : p.A + (kbeg + (int64_t)kt * kBK) * p.lda; };
+  // A's base for k-tile kt (DmaOperand32: the offsets hold the rows and kbeg)
+  auto a_krow = [&](int kt) -> const bf16_t* {
+    return A_KC ? p.A + (int64_t)kt * kBK : p.A + (kbeg + (int64_t)kt * kBK) * p.lda;
+  };
+  auto b_issue = [&](int i, uint32_t dst, int kt, const bf16_t* bk) {
+    if constexpr (B_KC) db.issue_one(i, dst, kt, nullptr, wave);
+    else db.issue_one(i, dst, bk, wave);
+  };
   // LDS: A in three stages (tile t in stage t % 3), B in two (t % 2), 160 KB in all.  The A stage
   // of tile kt+2 is free from tile kt-1's barrier on, so its loads spread over k-steps 0..2 of
   // tile kt; only B's wait for tile kt's own barrier.  (The DMA path moves about 64 B per clock
@@ -956,9 +1003,9 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
     const bf16_t* ak = a_krow(kt);
     const bf16_t* bk = next_b();
 #pragma unroll
-    for (int i = 0; i < DA::PER; ++i) da.issue_one(i, a_lds(kt % 3), kt, ak, wave);
+    for (int i = 0; i < DA::PER; ++i) da.issue_one(i, a_lds(kt % 3), ak, wave);
 #pragma unroll
-    for (int i = 0; i < DB::PER; ++i) db.issue_one(i, b_lds(kt & 1), kt, bk, wave);
+    for (int i = 0; i < DB::PER; ++i) b_issue(i, b_lds(kt & 1), kt, bk);
   };
 
   floatx16_t acc[FM][FN];
@@ -1012,7 +1059,7 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
         if (RH_W4_SPREAD ? (t % 2 == 0) : (t < FM + FN)) frag((ks + 1) & 1, sa, sb, ks + 1, frag_order(RH_W4_SPREAD ? t / 2 : t));
         if constexpr (REFILL) {
           const int g = ks * 16 + t;  // A windows of tile kt+2 at MFMA slots 3, 9, ..., 45
-          if (g % 6 == 3) da.issue_one(g / 6, a_lds(fa3), kt + 2, ak, wave);
+          if (g % 6 == 3) da.issue_one(g / 6, a_lds(fa3), ak, wave);
         }
       }
     }
@@ -1030,7 +1077,7 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
           frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, frag_order(RH_W4_SPREAD ? t / 2 : t));
       }
       if constexpr (REFILL) {
-        if (t % 2 == RH_W4_SPREAD) db.issue_one(t / 2, b_lds(kt & 1), kt + 2, bk, wave);
+        if (t % 2 == RH_W4_SPREAD) b_issue(t / 2, b_lds(kt & 1), kt + 2, bk);
       }
     }
   };
@@ -1467,6 +1514,26 @@ inline int validate(const rh_gemm_desc* d) {
   return RH_OK;
 }
 
+// Which kernel runs a 256x256 direct-to-LDS tile: the 4-wave one (gemm_dma_tile_w4) for grouped
+// launches (the weight gradients: long K, no epilogue), the 8-wave one for single GEMMs, whose
+// epilogues (GELU, residual) it finishes faster through LDS (measured inside the block's step).
+// RESIHP_GEMM_WAVES=4 or 8 pins one for both (tests run both).
+inline bool four_wave_256(bool grouped) {
+  const char* e = getenv("RESIHP_GEMM_WAVES");
+  if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] == '4';
+  return grouped;
+}
+
+// The 4-wave kernel addresses A (and an m/n-contiguous B) with 32-bit byte offsets from a
+// wave-uniform base (DmaOperand32): every offset it forms must stay below 2^32 bytes.
+inline bool w4_addressable(const rh_gemm_desc* d) {
+  constexpr int64_t kLim = (int64_t)1 << 31;  // elements
+  const bool a_kc = d->layout != RH_GEMM_TN, b_kc = d->layout == RH_GEMM_NT;
+  const int64_t a_span = a_kc ? d->M * d->lda + d->K : (int64_t)kBK * d->lda + d->M;
+  const int64_t b_span = b_kc ? 0 : (int64_t)kBK * d->ldb + d->N;
+  return a_span < kLim && b_span < kLim;
+}
+
 template <typename T>
 GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   GemmParams<T> p;
@@ -1506,6 +1573,7 @@ GemmParams<T> make_params(const rh_gemm_desc* d, const Plan& pl, void* ws) {
   // (epilogue_tile_impl checks the alignment of each 8-element chunk itself)
   const bool lds = pl.splits + pl.tail == 1 && d->epilogue != RH_EPI_GELU_GRAD && d->epilogue != RH_EPI_MUL_AUX;
   p.epi_lds = lds ? 1 : 0;
+  p.w4 = w4_addressable(d) ? 1 : 0;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   // Each XCD receives a contiguous run of ~tiles/8 logical tiles (tile_coords); grouping that
@@ -1525,21 +1593,12 @@ void launch_bf16(const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t s
   else hipLaunchKernelGGL((gemm_bf16_mfma<BM, BN, WGM, WGN, L, EPI, SPLIT>), grid, dim3(64 * WGM * WGN), 0, st, p);
 }
 
-// Which kernel runs a 256x256 direct-to-LDS tile: the 4-wave one (gemm_dma_tile_w4) for grouped
-// launches (the weight gradients: long K, no epilogue), the 8-wave one for single GEMMs, whose
-// epilogues (GELU, residual) it finishes faster through LDS (measured inside the block's step).
-// RESIHP_GEMM_WAVES=4 or 8 pins one for both (tests run both).
-inline bool four_wave_256(bool grouped) {
-  const char* e = getenv("RESIHP_GEMM_WAVES");
-  if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] == '4';
-  return grouped;
-}
 
 template <int L, int EPI, bool SPLIT>
 void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t st) {
   switch (cfg) {
     case kT256x256:
-      if (dma && four_wave_256(false))
+      if (dma && four_wave_256(false) && p.w4)
         hipLaunchKernelGGL((gemm_bf16_dma<256, 256, 2, 2, L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
       else launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st);
       break;
@@ -1710,20 +1769,25 @@ int launch_grouped(const rh_gemm_desc* d, int n, const GroupPlan& g, void* ws, h
   gp.first[n] = total;
   gp.count = n;
   gp.splits = g.splits;
-  if (four_wave_256(true)) {
+  const unsigned grid = (unsigned)total;
+  bool w4 = four_wave_256(true);
+  for (int i = 0; i < n; ++i) w4 = w4 && w4_addressable(&d[i]);
+  if (w4) {
     if (g.splits > 1)
-      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, true>), dim3((unsigned)total), dim3(256), 0, st, gp);
+      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, true>), dim3(grid), dim3(256), 0, st, gp);
     else
-      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, false>), dim3((unsigned)total), dim3(256), 0, st, gp);
+      hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 2, L, false>), dim3(grid), dim3(256), 0, st, gp);
   } else if (g.splits > 1)
-    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, true>), dim3((unsigned)total), dim3(512), 0, st, gp);
+    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, true>), dim3(grid), dim3(512), 0, st, gp);
   else
-    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, false>), dim3((unsigned)total), dim3(512), 0, st, gp);
+    hipLaunchKernelGGL((gemm_bf16_dma_grouped<256, 256, 2, 4, L, false>), dim3(grid), dim3(512), 0, st, gp);
   int rc = rh_check_launch("rh_gemm_grouped");
-  if (rc || g.splits == 1) return rc;
-  for (int i = 0; i < n; ++i) {
-    rc = launch_reduce<bf16_t, RH_EPI_NONE>(&d[i], gp.p[i], g.splits, gp.p[i].ws, st);
-    if (rc) return rc;
+  if (rc) return rc;
+  if (g.splits > 1) {
+    for (int i = 0; i < n; ++i) {
+      rc = launch_reduce<bf16_t, RH_EPI_NONE>(&d[i], gp.p[i], g.splits, gp.p[i].ws, st);
+      if (rc) return rc;
+    }
   }
   return RH_OK;
 }
