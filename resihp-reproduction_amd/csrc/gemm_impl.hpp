@@ -1035,9 +1035,6 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
 #pragma unroll
     for (int f = 0; f < FM + FN; ++f) frag(0, a_ptr(0), b_ptr(0), 0, f);
   }
-#ifndef RH_W4_SPREAD
-#define RH_W4_SPREAD 1
-#endif
   // Fragment reads, one every other MFMA, in the order the next k-step's MFMAs (row-major over
   // the 4 x 4 accumulator blocks) first need them: A0, B0..B3, A1, A2, A3.
   auto frag_order = [](int slot) { return slot == 0 ? 0 : slot < 5 ? FM + slot - 1 : slot - 4; };
@@ -1056,7 +1053,7 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
 #pragma unroll
       for (int t = 0; t < FM * FN; ++t) {
         mfma_agpr(acc[t / FN][t % FN], fa[ks & 1][t / FN], fb[ks & 1][t % FN]);
-        if (RH_W4_SPREAD ? (t % 2 == 0) : (t < FM + FN)) frag((ks + 1) & 1, sa, sb, ks + 1, frag_order(RH_W4_SPREAD ? t / 2 : t));
+        if (t % 2 == 0) frag((ks + 1) & 1, sa, sb, ks + 1, frag_order(t / 2));
         if constexpr (REFILL) {
           const int g = ks * 16 + t;  // A windows of tile kt+2 at MFMA slots 3, 9, ..., 45
           if (g % 6 == 3) da.issue_one(g / 6, a_lds(fa3), ak, wave);
@@ -1073,11 +1070,10 @@ __device__ __forceinline__ void gemm_dma_tile_w4(const GemmParams<bf16_t>& p, bf
     for (int t = 0; t < FM * FN; ++t) {
       mfma_agpr(acc[t / FN][t % FN], fa[1][t / FN], fb[1][t % FN]);
       if constexpr (MORE) {
-        if (RH_W4_SPREAD ? (t % 2 == 0) : (t < FM + FN))
-          frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, frag_order(RH_W4_SPREAD ? t / 2 : t));
+        if (t % 2 == 0) frag(0, a_ptr(na3), b_ptr((kt + 1) & 1), 0, frag_order(t / 2));
       }
       if constexpr (REFILL) {
-        if (t % 2 == RH_W4_SPREAD) b_issue(t / 2, b_lds(kt & 1), kt + 2, bk);
+        if (t % 2 == 1) b_issue(t / 2, b_lds(kt & 1), kt + 2, bk);  // between the reads
       }
     }
   };
