@@ -98,7 +98,7 @@ extern "C" int rh_gemm_kernel_name(const rh_gemm_desc* desc, char* buf, int64_t 
   }
   const GemmParams<bf16_t> p = make_params<bf16_t>(desc, pl, nullptr);
   const bool dma = dma_ok(desc, pl, p);
-  const bool w4 = dma && pl.cfg == kT256x256 && four_wave_256(false) && p.w4;  // as launch_cfg decides
+  const bool w4 = dma && pl.cfg == kT256x256 && four_wave_256(pl.splits > 1) && p.w4;  // as launch_cfg decides
   snprintf(buf, (size_t)len, "%s<%d, %d, %d, %d, %d, %d, %s>", dma ? "gemm_bf16_dma" : "gemm_bf16_mfma",
            kShapes[pl.cfg].bm, kShapes[pl.cfg].bn, kWaves[pl.cfg][0], w4 ? 2 : kWaves[pl.cfg][1], desc->layout,
            pl.splits + pl.tail > 1 ? 0 : desc->epilogue,  // split slices use the RH_EPI_NONE kernels

@@ -1511,13 +1511,14 @@ inline int validate(const rh_gemm_desc* d) {
 }
 
 // Which kernel runs a 256x256 direct-to-LDS tile: the 4-wave one (gemm_dma_tile_w4) for grouped
-// launches (the weight gradients: long K, no epilogue), the 8-wave one for single GEMMs, whose
-// epilogues (GELU, residual) it finishes faster through LDS (measured inside the block's step).
-// RESIHP_GEMM_WAVES=4 or 8 pins one for both (tests run both).
-inline bool four_wave_256(bool grouped) {
+// launches and split-K slices (the weight gradients and the LM head's dgrad: long K, fp32 partials
+// or no epilogue; the GPT-2-small head dgrad runs 0.64 ms instead of 0.87), the 8-wave one for unsplit
+// single GEMMs, whose epilogues (GELU, residual) it finishes faster through LDS (measured inside the
+// block's step).  RESIHP_GEMM_WAVES=4 or 8 pins one for all (tests run both).
+inline bool four_wave_256(bool long_k) {
   const char* e = getenv("RESIHP_GEMM_WAVES");
   if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] == '4';
-  return grouped;
+  return long_k;
 }
 
 // The 4-wave kernel addresses A (and an m/n-contiguous B) with 32-bit byte offsets from a
@@ -1594,7 +1595,7 @@ template <int L, int EPI, bool SPLIT>
 void launch_cfg(int cfg, const GemmParams<bf16_t>& p, bool dma, dim3 grid, hipStream_t st) {
   switch (cfg) {
     case kT256x256:
-      if (dma && four_wave_256(false) && p.w4)
+      if (dma && four_wave_256(SPLIT) && p.w4)
         hipLaunchKernelGGL((gemm_bf16_dma<256, 256, 2, 2, L, EPI, SPLIT>), grid, dim3(256), 0, st, p);
       else launch_bf16<256, 256, 2, 4, L, EPI, SPLIT>(p, dma, grid, st);
       break;

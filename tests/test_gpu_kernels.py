@@ -42,17 +42,17 @@ SHAPES = [(128, 128, 64), (256, 384, 512), (100, 77, 50), (33, 200, 129), (1, 8,
           (256, 384, 1000)]  # ragged K with aligned M/N: direct-to-LDS bulk + register-staged K tail
 
 
-@pytest.fixture(params=["auto", "0", "0w4", "1", "2", "3"])
+@pytest.fixture(params=["auto", "0", "0w4", "0w8", "1", "2", "3"])
 def gemm_tile(request, monkeypatch):
     """Pin the bf16 GEMM tile shape (256x256 / 256x128 / 128x128 / 256x192, the last for NT
-    only) or let the planner choose; "0w4" is 256x256 on the 4-wave kernel instead of the 8-wave
-    one."""
+    only) or let the planner choose; "0w4" / "0w8" run every 256x256 tile on the 4-wave / 8-wave
+    kernel (by default unsplit single GEMMs take the 8-wave one, split-K slices the 4-wave one)."""
     monkeypatch.delenv("RESIHP_GEMM_WAVES", raising=False)
     if request.param == "auto":
         monkeypatch.delenv("RESIHP_GEMM_TILE", raising=False)
-    elif request.param == "0w4":
+    elif request.param in ("0w4", "0w8"):
         monkeypatch.setenv("RESIHP_GEMM_TILE", "0")
-        monkeypatch.setenv("RESIHP_GEMM_WAVES", "4")
+        monkeypatch.setenv("RESIHP_GEMM_WAVES", request.param[-1])
     else:
         monkeypatch.setenv("RESIHP_GEMM_TILE", request.param)
     return request.param
