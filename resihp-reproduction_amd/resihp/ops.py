@@ -644,7 +644,8 @@ class _NextTokenLossFn(torch.autograd.Function):
         lse = torch.empty(rows, dtype=torch.float32, device=dev)
         loss = torch.empty((), dtype=torch.float32, device=dev)
         dl = None
-        if torch.is_grad_enabled() and logits.requires_grad:
+        # (grad mode is off inside Function.forward; needs_input_grad says whether backward will run)
+        if ctx.needs_input_grad[0]:
             ld_d = (vocab + 7) // 8 * 8
             dl = torch.empty((rows, ld_d), dtype=logits.dtype, device=dev)
         nbytes = H.query("rh_xent_workspace_bytes", batch, seq)
