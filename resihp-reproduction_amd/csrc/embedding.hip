@@ -95,7 +95,7 @@ __global__ __launch_bounds__(1024) void emb_bitonic_tile(uint64_t* __restrict__ 
   for (int64_t k = k_lo; k <= k_hi; k <<= 1) {
     for (int j = (int)min<int64_t>(k, tile) >> 1; j > 0; j >>= 1) {
       for (int t = threadIdx.x; t < tile / 2; t += 1024) {
-        const int i = (t / j) * 2 * j + (t % j);  // i has bit j clear; its partner is i + j
+        const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));  // i has bit j clear (j a power of two); partner i + j
         const uint64_t a = sk[i], b = sk[i + j];
         const bool up = ((base + i) & k) == 0;
         if (up ? (a > b) : (a < b)) {
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(1024) void emb_bitonic_tile(uint64_t* __restrict__ 
 // One bitonic compare distance j >= tile of stage k, over global memory.
 __global__ __launch_bounds__(256) void emb_bitonic_global(uint64_t* __restrict__ keys, int64_t N, int64_t k, int64_t j) {
   for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < N / 2; t += (int64_t)gridDim.x * 256) {
-    const int64_t i = (t / j) * 2 * j + (t % j);
+    const int64_t i = ((t & ~(j - 1)) << 1) | (t & (j - 1));  // j a power of two
     const uint64_t a = keys[i], b = keys[i + j];
     const bool up = (i & k) == 0;
     if (up ? (a > b) : (a < b)) {
@@ -129,13 +129,15 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(int64_t n, T* p) {
 
 __device__ __forceinline__ uint64_t key_id(uint64_t k) { return k >> 32; }
 
-// Level 1 of the per-id sum: workgroup c sums the sorted rows [32c, 32c + 32) per id, each
-// thread over its own columns (all 32 row loads of a column issued before the sums).  Piece
+// Level 1 of the per-id sum: workgroup (c, y) sums the sorted rows [32c, 32c + 32) per id over
+// columns 64y .. 64y+63, one column per lane (all 32 row loads issued before the sums, then all
+// gradient-row loads of the pieces that go straight into dW); one wave per workgroup and one
+// workgroup per (chunk, 64 columns), so the chip has enough loads in flight.  Piece
 // slots: head[c] holds the chunk's first piece when that id began in an earlier chunk; tail[c]
 // its last piece when that id continues into the next chunk and began in this one.  Pieces
 // closed on both sides go straight into dW.
 template <typename T>
-__global__ __launch_bounds__(256) void emb_chunk_sum(int64_t n, int dim, const uint64_t* __restrict__ keys,
+__global__ __launch_bounds__(64) void emb_chunk_sum(int64_t n, int dim, const uint64_t* __restrict__ keys,
                                                       const T* __restrict__ dout, T* __restrict__ dW,
                                                       float* __restrict__ head, float* __restrict__ tail) {
   __shared__ uint64_t sk[kChunk + 2];  // keys of rows lo-1 .. hi (kNoKey outside [0, n))
@@ -148,34 +150,46 @@ __global__ __launch_bounds__(256) void emb_chunk_sum(int64_t n, int dim, const u
   }
   __syncthreads();
   if (sk[1] == kNoKey) return;
-  for (int col = threadIdx.x; col < dim; col += 256) {
-    float val[kChunk];
+  // which rows end a piece and where its sum goes (the same for every column): bit i of `direct` /
+  // `to_head` / `to_tail` marks the piece ending at row lo + i
+  uint32_t direct = 0, to_head = 0, to_tail = 0;
+  {
+    bool first_piece = true;
+    for (int i = 0; i < m; ++i) {
+      const uint64_t k = sk[i + 1];
+      if (k == kNoKey) break;
+      const uint64_t next = sk[i + 2];  // row lo + i + 1 (the next chunk's first row when i = m - 1)
+      const bool same_next = next != kNoKey && key_id(next) == key_id(k);
+      if (same_next && i + 1 < m) continue;  // the id goes on inside this chunk
+      const bool open_start = first_piece && sk[0] != kNoKey && key_id(sk[0]) == key_id(k);
+      if (open_start) to_head |= 1u << i;
+      else if (same_next) to_tail |= 1u << i;
+      else direct |= 1u << i;
+      first_piece = false;
+    }
+  }
+  const uint32_t live = direct | to_head | to_tail;
+  const int col = (int)blockIdx.y * 64 + (int)threadIdx.x;
+  if (col < dim) {
+    float val[kChunk], old[kChunk];
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
       const uint64_t k = sk[i + 1];
       val[i] = (i < m && k != kNoKey) ? ld_f32(dout + (int64_t)(k & 0xffffffffu) * dim + col) : 0.f;
     }
+    // the gradient rows the direct pieces add to, all loads issued before any is used
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i)
+      old[i] = (direct >> i) & 1u ? ld_f32(dW + (int64_t)key_id(sk[i + 1]) * dim + col) : 0.f;
     float acc = 0.f;
-    bool first_piece = true;
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
-      const uint64_t k = sk[i + 1];
-      if (i >= m || k == kNoKey) break;
       acc += val[i];
-      const uint64_t next = sk[i + 2];  // row lo + i + 1 (the next chunk's first row when i = m - 1)
-      const bool same_next = next != kNoKey && key_id(next) == key_id(k);
-      if (same_next && i + 1 < m) continue;  // the id goes on inside this chunk
-      const bool open_start = first_piece && sk[0] != kNoKey && key_id(sk[0]) == key_id(k);
-      if (open_start) {
-        head[c * dim + col] = acc;
-      } else if (same_next) {
-        tail[c * dim + col] = acc;
-      } else {
-        T* w = dW + (int64_t)key_id(k) * dim + col;
-        st_f32(w, ld_f32(w) + acc);
-      }
+      if (!((live >> i) & 1u)) continue;
+      if ((to_head >> i) & 1u) head[c * dim + col] = acc;
+      else if ((to_tail >> i) & 1u) tail[c * dim + col] = acc;
+      else st_f32(dW + (int64_t)key_id(sk[i + 1]) * dim + col, old[i] + acc);
       acc = 0.f;
-      first_piece = false;
     }
   }
 }
@@ -311,22 +325,27 @@ extern "C" int rh_embedding_bwd(int dtype, int64_t batch, int64_t seq, int64_t d
       // compare distances down to the tile size and one LDS launch for the rest
       const int tile = (int)std::min<int64_t>(N, kTile);
       const unsigned tiles = (unsigned)(N / tile);
-      hipLaunchKernelGGL(emb_bitonic_tile, dim3(tiles), dim3(1024), 0, st, keys, tile, (int64_t)2, (int64_t)tile);
+      // stages up to 1024 on 1024-key tiles (many workgroups at once), the rest on whole tiles
+      const int small = std::min(tile, 1024);
+      hipLaunchKernelGGL(emb_bitonic_tile, dim3((unsigned)(N / small)), dim3(1024), 0, st, keys, small, (int64_t)2,
+                         (int64_t)small);
+      if (tile > small)
+        hipLaunchKernelGGL(emb_bitonic_tile, dim3(tiles), dim3(1024), 0, st, keys, tile, (int64_t)(2 * small),
+                           (int64_t)tile);
       const unsigned gg = (unsigned)std::min<int64_t>(rh_cdiv(N / 2, 256), 65536);
       for (int64_t k = 2 * (int64_t)tile; k <= N; k <<= 1) {
         for (int64_t j = k >> 1; j >= tile; j >>= 1)
           hipLaunchKernelGGL(emb_bitonic_global, dim3(gg), dim3(256), 0, st, keys, N, k, j);
         hipLaunchKernelGGL(emb_bitonic_tile, dim3(tiles), dim3(1024), 0, st, keys, tile, k, k);
       }
-      const unsigned gc = (unsigned)chunks;
       const dim3 gj((unsigned)chunks, (unsigned)rh_cdiv(dim, 64));
       if (bf16) {
-        hipLaunchKernelGGL(emb_chunk_sum<bf16_t>, dim3(gc), dim3(256), 0, st, rows, (int)dim, keys,
+        hipLaunchKernelGGL(emb_chunk_sum<bf16_t>, gj, dim3(64), 0, st, rows, (int)dim, keys,
                            (const bf16_t*)dout, (bf16_t*)dtok, head, tail);
         hipLaunchKernelGGL(emb_chunk_join<bf16_t>, gj, dim3(256), 0, st, rows, (int)dim, keys, (bf16_t*)dtok,
                            head, tail);
       } else {
-        hipLaunchKernelGGL(emb_chunk_sum<float>, dim3(gc), dim3(256), 0, st, rows, (int)dim, keys,
+        hipLaunchKernelGGL(emb_chunk_sum<float>, gj, dim3(64), 0, st, rows, (int)dim, keys,
                            (const float*)dout, (float*)dtok, head, tail);
         hipLaunchKernelGGL(emb_chunk_join<float>, gj, dim3(256), 0, st, rows, (int)dim, keys, (float*)dtok, head,
                            tail);
