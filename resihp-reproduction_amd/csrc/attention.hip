@@ -487,27 +487,6 @@ struct RowDma {
   }
 };
 
-// The same tile load with the compiler's own direct-to-LDS builtin and per-lane 64-bit
-// addresses.  The compiler tracks these loads and waits for them before the first LDS read that
-// may alias the tile -- in the forward and dQ kernels that is the transposed-operand read of the
-// current stage, so the next stage's K/V land while the scores and softmax are computed.  Measured
-// on MI355X (cfg3 shard, same box): forward 48 us and dQ 62 us this way against 56 us and 73 us
-// with RowDma's explicit loads; dK/dV is the opposite (66 us with RowDma, 75 us this way).
-template <int D>
-__device__ __forceinline__ void dma_rows(bf16_t* tile, const bf16_t* base, int64_t ld, int r0, int last, int wave,
-                                         int lane) {
-  constexpr int CPR = D / 8, RPW = 64 / CPR, WINDOWS = kStageRows / RPW;
-  static_assert(WINDOWS % 8 == 0, "tile windows must split evenly over 8 waves");
-#pragma unroll
-  for (int i = 0; i < WINDOWS / 8; ++i) {
-    const int win = wave + 8 * i;
-    const int row = win * RPW + lane / CPR;
-    const int grow = min(r0 + row, last);
-    const bf16_t* src = base + (int64_t)grow * ld + (RowDma<D>::sw_chunk(row, lane % CPR) << 3);
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(tile + win * 512), 16, 0, 0);
-  }
-}
-
 __device__ __forceinline__ void wait_vm() { wait_vm_le<0>(); }
 
 // Store 4 consecutive head-dim values (registers 4rr..4rr+3) as bf16.
@@ -630,12 +609,14 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
   constexpr uint32_t TB = 2 * TILE;  // bytes per tile
   __shared__ __attribute__((aligned(256))) bf16_t smem[4 * TILE];  // K slots 0, 1 then V slots 0, 1
   __shared__ float mbuf[2][kPhases][2][64];                         // m and lsum of every wave
+  __shared__ __attribute__((aligned(256))) bf16_t sQ[64 * D];       // the item's 64 query rows
   static_assert(kPhases * 64 * D * 4 <= 4 * TILE * 2, "merge buffer must fit the stages");
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in an SGPR
   const int sub = w & 1, ph = w >> 1;
   const FragAddr<D> fa(lane);
   const RowDma<D> dma(a.ld_qkv, w, lane);
+  const RowDma<D, 64> qdma(a.ld_qkv, w, lane);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
   const uint32_t ks0 = lds_addr(smem), vs0 = ks0 + 2 * TB;
@@ -654,8 +635,10 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
     const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
     const int nst = (kv_end + kStageRows - 1) / kStageRows;
 
-    bf16x8_t qreg[KS];
-    load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, q_row < S, g);
+    // The Q rows come through LDS like K and V (rows past S repeat row S-1; their results are
+    // never stored): with no register loads in flight the compiler places no wait of its own,
+    // whose count would also cover V(0) and K(1) and hold the first scores until those landed.
+    qdma.issue(sQ, a.q + tok0 * a.ld_qkv + (int64_t)h * D, it.blk * 64, S - 1, w, lane);
     dma.issue(ks0, kbase, 0, S - 1, w, lane);
     dma.issue(vs0, vbase, 0, S - 1, w, lane);
     if (nst > 1) {
@@ -665,6 +648,9 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
       wait_vm_le<RowDma<D>::PER>();
     }
     __syncthreads();
+    bf16x8_t qreg[KS];
+#pragma unroll
+    for (int i = 0; i < KS; ++i) qreg[i] = row_frag<D>(sQ, 32 * sub, i, fa);
     floatx16_t oacc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) oacc[d] = zero16();
@@ -825,6 +811,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
   float* cbuf = reinterpret_cast<float*>(smem);
+  // K and V stages load with explicit direct-to-LDS loads awaited by the loop's own wait at the
+  // stage barrier; the compiler's waits (which would also count them) stay in the item prologue.
+  const RowDma<D> kvdma(a.ld_qkv, w, lane);
 
   for (int pass = 0; pass < 2; ++pass) {
     const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
@@ -840,8 +829,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
     const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
     const int nst = (kv_end + kStageRows - 1) / kStageRows;
-    dma_rows<D>(smem, kbase, a.ld_qkv, 0, S - 1, w, lane);
-    dma_rows<D>(smem + TILE, vbase, a.ld_qkv, 0, S - 1, w, lane);
+    kvdma.issue(smem, kbase, 0, S - 1, w, lane);
+    kvdma.issue(smem + TILE, vbase, 0, S - 1, w, lane);
 
     bf16x8_t qreg[KS], doreg[KS];
     load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, qok, g);
@@ -869,12 +858,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
 #pragma unroll
     for (int d = 0; d < DB; ++d) dqt[d] = zero16();
     wait_vm();
+    // Q and dO rows are in (the wait above covers every load): consumed here so the compiler's
+    // own wait for them is not placed inside the loop, where it would also count the next
+    // stage's loads (as in the dK/dV kernel).
+#pragma unroll
+    for (int i = 0; i < KS; ++i) asm volatile("" ::"v"(qreg[i]), "v"(doreg[i]));
     __syncthreads();
     for (int t = 0; t < nst; ++t) {
       if (t + 1 < nst) {
         bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
-        dma_rows<D>(nxt, kbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
-        dma_rows<D>(nxt + TILE, vbase, a.ld_qkv, (t + 1) * kStageRows, S - 1, w, lane);
+        kvdma.issue(nxt, kbase, (t + 1) * kStageRows, S - 1, w, lane);
+        kvdma.issue(nxt + TILE, vbase, (t + 1) * kStageRows, S - 1, w, lane);
       }
       const bf16_t* sK = smem + (t & 1) * 2 * TILE;
       const bf16_t* sV = sK + TILE;
@@ -959,37 +953,37 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
     const float* dlt = a.delta + (int64_t)it.bh * S;
     const int q_start = a.causal ? it.blk * 64 : 0;
     const int nst = (S - q_start + kStageRows - 1) / kStageRows;
-    float l_pref = 0.f, d_pref = 0.f;
-    auto fetch_stats = [&](int q0) {
-      if (tid < kStageRows) {
-        const int q = q0 + tid;
-        l_pref = q < S ? lse[q] * kLog2e : 0.f;
-        d_pref = q < S ? dlt[q] : 0.f;
-      }
-    };
-    auto put_stats = [&](int stage) {
-      if (tid < kStageRows) {
-        sL[stage][tid] = l_pref;
-        sDel[stage][tid] = d_pref;
+    // A stage's lse and delta go global->LDS like its Q and dO rows (waves 0 and 1, one query per
+    // lane; queries past S read row S-1, whose results are masked), so the loop holds no load in
+    // registers: a register load there makes the compiler wait on vmcnt inside the stage, and that
+    // count also covers the next stage's direct-to-LDS loads, which would then land before the
+    // stage computes instead of behind it.
+    auto stats_dma = [&](int q0, int slot) {
+      if (w < 2) {
+        const uint32_t off = (uint32_t)(4 * min(q0 + tid, S - 1));
+        dma4s(lse, off, lds_addr(&sL[slot][64 * w]));
+        dma4s(dlt, off, lds_addr(&sDel[slot][64 * w]));
       }
     };
     const RowDma<D> qdma(a.ld_qkv, w, lane), ddma(a.ld_do, w, lane);
     qdma.issue(smem, qbase, q_start, S - 1, w, lane);
     ddma.issue(smem + TILE, dbase, q_start, S - 1, w, lane);
-    fetch_stats(q_start);
-    put_stats(0);
+    stats_dma(q_start, 0);
     wait_vm();
+    // The K rows have landed (the wait above covers every load); the compiler does not read
+    // that from the asm, so the rows are consumed here, where its own wait for them is free,
+    // rather than at their first use inside the loop, where its wait would count the next
+    // stage's loads too.
+#pragma unroll
+    for (int i = 0; i < KS; ++i) asm volatile("" ::"v"(kreg[i]));
     __syncthreads();
     for (int t = 0; t < nst; ++t) {
       const int q0 = q_start + t * kStageRows;
-      // next stage's lse / delta: fetched and stored on every iteration (a stage past the end
-      // only fills the idle slot), so no load is ever outstanding across the loop back edge
-      // and the compiler's wait for them stays at put_stats
-      fetch_stats(q0 + kStageRows);
       if (t + 1 < nst) {
         bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
         qdma.issue(nxt, qbase, q0 + kStageRows, S - 1, w, lane);
         ddma.issue(nxt + TILE, dbase, q0 + kStageRows, S - 1, w, lane);
+        stats_dma(q0 + kStageRows, (t + 1) & 1);
       }
       const int cur = t & 1;
       const bf16_t* sQ = smem + cur * 2 * TILE;
@@ -1026,7 +1020,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
             const int r = 4 * r4 + j;
             const int q = q0 + qi0 + j;
             const bool ok = !ragged || (q < S && key < S && !(diag && key > q));
-            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lq[j])) : 0.f;
+            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lq[j] * kLog2e)) : 0.f;
             dp[r] = p * (dp[r] - dq4[j]);
             sc[r] = p;
           }
@@ -1050,7 +1044,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
           }
         }
       }
-      put_stats(cur ^ 1);
       wait_vm();
       __syncthreads();
     }

@@ -199,6 +199,22 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
       : "memory", "m0");
 }
 
+// The 4-byte form: lane l fetches the dword at sbase + voff into LDS byte lds_dst + 4*l.
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_dst);
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 4\n\t"
+      "global_load_lds_dword %0, %1"
+      :
+      : "v"(voff), "s"(sb), "s"(lds)
+      : "memory", "m0");
+}
+
 // wait until at most N of this thread's vector-memory loads (direct-to-LDS ones included) are
 // outstanding; they complete in issue order
 template <int N>

@@ -56,7 +56,8 @@ def test_library_version_and_argument_errors():
 
 def test_gemm_kernel_name_reports_the_planned_instantiation():
     """Planning needs no GPU (an absent device counts as 256 CUs): the wgrad of the 1.3B shard's
-    fc layers is a split-K direct-to-LDS TN GEMM, a ragged fp32 GEMM the FMA kernel."""
+    fc layers is a split-K direct-to-LDS TN GEMM (split slices run on the 4-wave 256x256 tile, unsplit
+    single GEMMs on the 8-wave one), a ragged fp32 GEMM the FMA kernel."""
     def name(dtype, layout, M, N, K, align=16, lda=None):
         d = _hip.rh_gemm_desc()
         d.dtype, d.layout, d.M, d.N, d.K = dtype, layout, M, N, K
@@ -70,7 +71,7 @@ def test_gemm_kernel_name_reports_the_planned_instantiation():
         _hip.call("rh_gemm_kernel_name", ctypes.byref(d), buf, 128)
         return buf.value.decode()
 
-    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_TN, 2048, 2048, 8192) == "gemm_bf16_dma<256, 256, 2, 4, 2, 0, true>"
+    assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_TN, 2048, 2048, 8192) == "gemm_bf16_dma<256, 256, 2, 2, 2, 0, true>"
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 2048, 2048) == "gemm_bf16_dma<256, 256, 2, 4, 0, 0, false>"
     # N = 1536 (the q|k|v projection): 256x192 tiles, exactly one per CU
     assert name(_hip.RH_DTYPE_BF16, _hip.RH_GEMM_NT, 8192, 1536, 2048) == "gemm_bf16_dma<256, 192, 4, 2, 0, 0, false>"
