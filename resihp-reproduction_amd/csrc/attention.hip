@@ -701,9 +701,14 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
       mxc = tile_row_max(nxt, c);
     };
     int t = 0;
-    for (; t + 1 < nst; ++t) {
-      interior(sa, sb, t, (uint32_t)(t & 1));
+    for (; t + 2 < nst; t += 2) {
+      interior(sa, sb, t, 0u);
+      interior(sb, sa, t + 1, 1u);
+    }
+    if (t + 1 < nst) {
+      interior(sa, sb, t, 0u);
       sa = sb;
+      ++t;
     }
     // the last stage: masks where a key can lie past the query (diagonal) or past S (tail)
     wait_vm_le<0>();
