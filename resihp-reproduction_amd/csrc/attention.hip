@@ -1015,6 +1015,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
         }
         const bool diag = a.causal && qt0 < wk0 + 31;
         const bool ragged = diag || qt0 + 31 >= S || wk0 + 31 >= S;  // any element masked
+        // Masked scores become -inf (so p = 2^-inf = 0 and dS = 0; lse and delta are finite for
+        // every row read) and every stage runs one straight-line softmax body.  Selecting p per
+        // element instead makes the compiler branch around each exponential, and that exec-mask
+        // juggling (about 8 scalar instructions per score) ran on every stage.
+        if (ragged) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int q = q0 + 32 * ph + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (!(q < S && key < S && !(diag && key > q))) sc[r] = -INFINITY;
+          }
+        }
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int qi0 = 32 * ph + 8 * r4 + 4 * g;
@@ -1023,9 +1034,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * r4 + j;
-            const int q = q0 + qi0 + j;
-            const bool ok = !ragged || (q < S && key < S && !(diag && key > q));
-            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lq[j] * kLog2e)) : 0.f;
+            const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], c, -lq[j] * kLog2e));
             dp[r] = p * (dp[r] - dq4[j]);
             sc[r] = p;
           }
