@@ -617,6 +617,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
   const FragAddr<D> fa(lane);
   const RowDma<D> dma(a.ld_qkv, w, lane);
   const RowDma<D, 64> qdma(a.ld_qkv, w, lane);
+  const uint32_t sq0 = lds_addr(sQ);
   const int S = a.S, H = a.H, BH = a.B * a.H, nqb = (S + 63) / 64;
   const float c = a.scale * kLog2e;
   const uint32_t ks0 = lds_addr(smem), vs0 = ks0 + 2 * TB;
@@ -638,7 +639,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma(AttnArgs<bf16_t> a, int nit
     // The Q rows come through LDS like K and V (rows past S repeat row S-1; their results are
     // never stored): with no register loads in flight the compiler places no wait of its own,
     // whose count would also cover V(0) and K(1) and hold the first scores until those landed.
-    qdma.issue(sQ, a.q + tok0 * a.ld_qkv + (int64_t)h * D, it.blk * 64, S - 1, w, lane);
+    qdma.issue(sq0, a.q + tok0 * a.ld_qkv + (int64_t)h * D, it.blk * 64, S - 1, w, lane);
     dma.issue(ks0, kbase, 0, S - 1, w, lane);
     dma.issue(vs0, vbase, 0, S - 1, w, lane);
     if (nst > 1) {
@@ -819,6 +820,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
   // K and V stages load with explicit direct-to-LDS loads awaited by the loop's own wait at the
   // stage barrier; the compiler's waits (which would also count them) stay in the item prologue.
   const RowDma<D> kvdma(a.ld_qkv, w, lane);
+  const uint32_t s0 = lds_addr(smem);  // stage st's K at s0 + 4*TILE*st bytes, its V 2*TILE bytes on
 
   for (int pass = 0; pass < 2; ++pass) {
     const int item = pass == 0 ? (int)blockIdx.x : nitems - 1 - (int)blockIdx.x;
@@ -834,8 +836,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     const bf16_t* vbase = a.v + tok0 * a.ld_qkv + (int64_t)h * D;
     const int kv_end = a.causal ? min(S, it.blk * 64 + 64) : S;
     const int nst = (kv_end + kStageRows - 1) / kStageRows;
-    kvdma.issue(smem, kbase, 0, S - 1, w, lane);
-    kvdma.issue(smem + TILE, vbase, 0, S - 1, w, lane);
+    kvdma.issue(s0, kbase, 0, S - 1, w, lane);
+    kvdma.issue(s0 + 2 * TILE, vbase, 0, S - 1, w, lane);
 
     bf16x8_t qreg[KS], doreg[KS];
     load_head_row<KS>(qreg, a.q + (tok0 + q_row) * a.ld_qkv + (int64_t)h * D, qok, g);
@@ -871,9 +873,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
     __syncthreads();
     for (int t = 0; t < nst; ++t) {
       if (t + 1 < nst) {
-        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+        const uint32_t nxt = s0 + (uint32_t)(((t + 1) & 1) * 4 * TILE);
         kvdma.issue(nxt, kbase, (t + 1) * kStageRows, S - 1, w, lane);
-        kvdma.issue(nxt + TILE, vbase, (t + 1) * kStageRows, S - 1, w, lane);
+        kvdma.issue(nxt + 2 * TILE, vbase, (t + 1) * kStageRows, S - 1, w, lane);
       }
       const bf16_t* sK = smem + (t & 1) * 2 * TILE;
       const bf16_t* sV = sK + TILE;
@@ -947,7 +949,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
     bf16x8_t kreg[KS];
     load_head_row<KS>(kreg, a.k + (tok0 + key) * a.ld_qkv + (int64_t)h * D, key < S, g);
     // V stays in LDS (registers are the binding limit at two waves per SIMD)
-    RowDma<D, 64>(a.ld_qkv, w, lane).issue(sVb, a.v + tok0 * a.ld_qkv + (int64_t)h * D, it.blk * 64, S - 1, w, lane);
+    RowDma<D, 64>(a.ld_qkv, w, lane).issue(lds_addr(sVb), a.v + tok0 * a.ld_qkv + (int64_t)h * D, it.blk * 64, S - 1, w, lane);
     floatx16_t acc[2 * DB];  // dK^T blocks 0..DB-1, dV^T blocks DB..2DB-1
 #pragma unroll
     for (int d = 0; d < 2 * DB; ++d) acc[d] = zero16();
@@ -971,8 +973,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
       }
     };
     const RowDma<D> qdma(a.ld_qkv, w, lane), ddma(a.ld_do, w, lane);
-    qdma.issue(smem, qbase, q_start, S - 1, w, lane);
-    ddma.issue(smem + TILE, dbase, q_start, S - 1, w, lane);
+    const uint32_t s0 = lds_addr(smem);  // stage st's Q at s0 + 4*TILE*st bytes, its dO 2*TILE bytes on
+    qdma.issue(s0, qbase, q_start, S - 1, w, lane);
+    ddma.issue(s0 + 2 * TILE, dbase, q_start, S - 1, w, lane);
     stats_dma(q_start, 0);
     wait_vm();
     // The K rows have landed (the wait above covers every load); the compiler does not read
@@ -985,9 +988,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_mfma(AttnArgs<bf16_t> a, in
     for (int t = 0; t < nst; ++t) {
       const int q0 = q_start + t * kStageRows;
       if (t + 1 < nst) {
-        bf16_t* nxt = smem + ((t + 1) & 1) * 2 * TILE;
+        const uint32_t nxt = s0 + (uint32_t)(((t + 1) & 1) * 4 * TILE);
         qdma.issue(nxt, qbase, q0 + kStageRows, S - 1, w, lane);
-        ddma.issue(nxt + TILE, dbase, q0 + kStageRows, S - 1, w, lane);
+        ddma.issue(nxt + 2 * TILE, dbase, q0 + kStageRows, S - 1, w, lane);
         stats_dma(q0 + kStageRows, (t + 1) & 1);
       }
       const int cur = t & 1;
