@@ -875,6 +875,10 @@ struct DmaOperand {
 #pragma unroll
     for (int i = 0; i < PER; ++i) issue_one(i, dst, kt, krow0, wave);
   }
+  __device__ __forceinline__ void issue(uint32_t dst, int kt, const bf16_t* krow0, int wave) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) issue_one(i, dst, kt, krow0, wave);
+  }
   __device__ __forceinline__ void issue_one(int i, bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
     const int win = wave + NWAVES * i;
     dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + win * 512);
@@ -1132,15 +1136,18 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmParams<bf16_t>& p, bf16_
     iss_seg = (int)kbeg / bseg_rows;
     iss_row = (int)kbeg - iss_seg * bseg_rows;
   }
+  // stages addressed as LDS byte offsets from one base converted once (a generic-to-LDS pointer
+  // conversion per load costs a null check in scalar instructions)
+  const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)smem;
   auto issue = [&](int kt) {
-    bf16_t* st = smem + (kt & 1) * STAGE;
+    const uint32_t st = sbase + (uint32_t)((kt & 1) * STAGE * 2);
     const int64_t k0 = kbeg + (int64_t)kt * kBK;
     da.issue(st, kt, A_KC ? nullptr : p.A + k0 * p.lda, wave);
     if (B_KC) {
-      db.issue(st + A_ELEMS, kt, nullptr, wave);
+      db.issue(st + A_ELEMS * 2, kt, nullptr, wave);
     } else {
       const bf16_t* base = iss_seg == 0 ? bs0 : iss_seg == 1 ? bs1 : iss_seg == 2 ? bs2 : bs3;
-      db.issue(st + A_ELEMS, kt, base + (int64_t)iss_row * p.ldb, wave);
+      db.issue(st + A_ELEMS * 2, kt, base + (int64_t)iss_row * p.ldb, wave);
       iss_row += kBK;
       if (iss_row >= bseg_rows) {
         iss_row -= bseg_rows;
