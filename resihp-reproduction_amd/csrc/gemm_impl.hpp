@@ -101,6 +101,27 @@ struct GemmParams {
 constexpr int kEpiLsePartial = 16;
 constexpr int kEpiXentGrad = 17;
 
+// Row r of a segmented result: the segment by comparisons (at most RH_MAX_SEG - 1 of them) rather
+// than a division, which is a long scalar/vector sequence for 64-bit values, and the epilogues
+// form one per output row.  The segment bases pass through an empty asm so the compiler keeps the
+// selects instead of re-forming a per-lane indexed read of the argument array (which it would
+// place in scratch memory).  (b_row runs once per tile in the loaders' set-up and keeps the
+// division.)
+template <typename P>
+__device__ __forceinline__ P seg_row(const P (&base)[RH_MAX_SEG], int nseg, int64_t seg, int64_t r, int64_t ld) {
+  if (nseg == 1) return base[0] + r * ld;
+  P b = base[0];
+#pragma unroll
+  for (int k = 1; k < RH_MAX_SEG; ++k) {
+    P bk = base[k];
+    asm volatile("" : "+s"(bk));
+    if (k < nseg && r >= seg) {
+      r -= seg;
+      b = bk;
+    }
+  }
+  return b + r * ld;
+}
 template <typename T>
 __device__ __forceinline__ const T* b_row(const GemmParams<T>& p, int64_t r) {
   if (p.b_nseg == 1) return p.B[0] + r * p.ldb;
@@ -109,9 +130,7 @@ __device__ __forceinline__ const T* b_row(const GemmParams<T>& p, int64_t r) {
 }
 template <typename T>
 __device__ __forceinline__ T* d_row(const GemmParams<T>& p, int64_t m) {
-  if (p.d_nseg == 1) return p.D[0] + m * p.ldd;
-  const int64_t s = m / p.d_seg;
-  return p.D[s] + (m - s * p.d_seg) * p.ldd;
+  return seg_row(p.D, p.d_nseg, p.d_seg, m, p.ldd);
 }
 
 // v = alpha*acc + beta*C ; epilogue ; store.  Shared by every GEMM kernel.
