@@ -577,28 +577,37 @@ __device__ __forceinline__ void epilogue_lse(const GemmParams<bf16_t>& p, floatx
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[j][t] = p.alpha * t4[t];
       }
-      int64_t tc = -1;
-      if (m < p.M && m % p.seq != p.seq - 1) tc = p.tokens[m + 1] - p.col_off;
-      float mx = -INFINITY;
+      // next-token id read unconditionally at a clamped (valid) index, then selected
+      const bool scored = m < p.M && m % p.seq != p.seq - 1;
+      const int64_t tn = p.tokens[min(m + 1, p.M - 1)];
+      const int64_t tc = scored ? tn - p.col_off : -1;
+      // Element loops without branches (columns past N are selected away; a per-element branch
+      // around each exponential costs exec-mask bookkeeping on every row): the lane holding the
+      // target column picks its logit by selects and stores it once.
+      float mx = -INFINITY, tv = 0.f;
+      bool has_t = false;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int64_t n = cl + j * 32 + t;
-          if (n < p.N) mx = fmaxf(mx, v[j][t] * kL2e);
-          if (n == tc) p.tgt[m] = v[j][t];
+          mx = fmaxf(mx, n < p.N ? v[j][t] * kL2e : -INFINITY);
+          tv = n == tc ? v[j][t] : tv;
+          has_t = has_t || n == tc;
         }
+      if (has_t) p.tgt[m] = tv;
       mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      // (a row with every column past N has mx = -inf: each term is then 2^inf, all selected away)
       float sum = 0.f;
-      if (mx != -INFINITY) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (cl + j * 32 + t < p.N) sum += __builtin_amdgcn_exp2f(fmaf(v[j][t], kL2e, -mx));
-      }
+        for (int t = 0; t < 4; ++t) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(v[j][t], kL2e, -mx));
+          sum += cl + j * 32 + t < p.N ? e : 0.f;
+        }
       sum += __shfl_xor(sum, 4, 64);
       sum += __shfl_xor(sum, 8, 64);
       sum += __shfl_xor(sum, 16, 64);
@@ -629,8 +638,12 @@ __device__ __forceinline__ void epilogue_xent_grad(const GemmParams<bf16_t>& p, 
     for (int q = 0; q < 4; ++q) {
       const int64_t m = rl + i * 32 + 8 * q;
       const bool scored = m < p.M && m % p.seq != p.seq - 1;
-      const int64_t tc = scored ? p.tokens[m + 1] - p.col_off : -1;
-      const float l2 = scored ? p.lse[m] * kL2e : 0.f;
+      // per-row values read unconditionally at clamped (valid) indices, then selected
+      const int64_t mc = min(m, p.M - 1);
+      const int64_t tn = p.tokens[min(m + 1, p.M - 1)];
+      const float lr = p.lse[mc];
+      const int64_t tc = scored ? tn - p.col_off : -1;
+      const float l2 = scored ? lr * kL2e : 0.f;
       bf16_t* drow = m < p.M ? d_row(p, m) : nullptr;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -641,10 +654,11 @@ __device__ __forceinline__ void epilogue_xent_grad(const GemmParams<bf16_t>& p, 
         u16x4_t o;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          float d = 0.f;
-          if (scored && n + t < p.N)
-            d = (__builtin_amdgcn_exp2f(fmaf(p.alpha * t4[t], kL2e, -l2)) - (n + t == tc ? 1.f : 0.f)) * scale;
-          o[t] = f32_to_bf16(d);
+          // computed for every element and selected (no branch per element; an unscored row's
+          // exponential may overflow, and the select drops it)
+          const float e = __builtin_amdgcn_exp2f(fmaf(p.alpha * t4[t], kL2e, -l2));
+          const float d = (e - (n + t == tc ? 1.f : 0.f)) * scale;
+          o[t] = f32_to_bf16(scored && n + t < p.N ? d : 0.f);
         }
         *reinterpret_cast<u16x4_t*>(drow + n) = o;
       }
