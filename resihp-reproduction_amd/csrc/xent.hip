@@ -4,10 +4,11 @@
 // One 256-thread block per logits row.  Pass 1 streams the row once with
 // 16-byte loads and keeps a per-thread online (max, sum-exp) pair, merged
 // across the block.  When the gradient is wanted in the same call, pass 2
-// re-reads the row (still resident in L2) and writes
-//   dlogits = (exp(x - lse) - [j == target]) / N
-// so the fused forward+backward moves 2 bytes in and 2 bytes out per bf16
-// logit.  Row losses are reduced to the mean by a single block in a fixed
+// re-reads the row and writes
+//   dlogits = (exp(x - lse) - [j == target]) / N.
+// bf16 rows of up to 65536 aligned logits take xent_fwd_grad_reg_kernel instead,
+// which holds the row in registers between the two passes, so the fused
+// forward+backward moves 2 bytes in and 2 bytes out per logit.  Row losses are reduced to the mean by a single block in a fixed
 // order (deterministic).
 #include "common.hpp"
 
@@ -151,6 +152,87 @@ __global__ __launch_bounds__(kT) void xent_fwd_kernel(int S, int64_t V, const T*
   if (dl) row_grad<T, VEC>(x, dl + row * ld_d, V, ld_d, lse, tgt, inv_n);
 }
 
+// bf16 rows of up to kRegCols logits with the gradient wanted in the same call: the row is read
+// once into registers (512 threads x 16 chunks of 8), its max and sum-exp come from the registers,
+// and the gradient is written from them, so the fused forward moves 2 bytes in and 2 bytes out per
+// logit with no second read of the row.  16-byte aligned rows (ld % 8 == 0).
+constexpr int kRT = 512, kRC = 16;
+constexpr int64_t kRegCols = (int64_t)kRT * kRC * 8;
+__global__ __launch_bounds__(kRT) void xent_fwd_grad_reg_kernel(int S, int64_t V, const bf16_t* __restrict__ logits,
+                                                                int64_t ld, const int64_t* __restrict__ tokens,
+                                                                float* __restrict__ lse_out, float* __restrict__ loss_rows,
+                                                                bf16_t* __restrict__ dl, int64_t ld_d, float inv_n) {
+  __shared__ float scratch[32];
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  bf16_t* drow = dl + row * ld_d;
+  if (s == S - 1) {
+    if (threadIdx.x == 0) {
+      loss_rows[row] = 0.f;
+      lse_out[row] = 0.f;
+    }
+    const u16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t j = (int64_t)threadIdx.x * 8; j < ld_d; j += kRT * 8) *reinterpret_cast<u16x8_t*>(drow + j) = z;
+    return;
+  }
+  const bf16_t* x = logits + row * ld;
+  const int64_t full = V / 8 * 8;
+  // chunk c of this thread: columns (c * kRT + tid) * 8 .. + 7; the last V % 8 columns (one per
+  // thread, tid < V % 8) in `tail`
+  u16x8_t raw[kRC];
+  float cm = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kRC; ++c) {
+    const int64_t j = ((int64_t)c * kRT + threadIdx.x) * 8;
+    raw[c] = u16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    if (j < full) raw[c] = *reinterpret_cast<const u16x8_t*>(x + j);
+  }
+  const int64_t jt = full + threadIdx.x;
+  const float tail = jt < V ? bf16_to_f32(x[jt]) : -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kRC; ++c) {
+    const int64_t j = ((int64_t)c * kRT + threadIdx.x) * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) cm = fmaxf(cm, j < full ? bf16_to_f32(raw[c][t]) : -INFINITY);
+  }
+  cm = fmaxf(cm, tail);
+  const float M2 = block_max(cm, scratch) * kLog2eX;  // row max, base-2 units
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < kRC; ++c) {
+    const int64_t j = ((int64_t)c * kRT + threadIdx.x) * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float e = exp2_hw(fmaf(bf16_to_f32(raw[c][t]), kLog2eX, -M2));
+      sum += j < full ? e : 0.f;
+    }
+  }
+  sum += jt < V ? exp2_hw(fmaf(tail, kLog2eX, -M2)) : 0.f;
+  const float tot = block_sum(sum, scratch + 16);
+  const float lse2 = M2 + log2f(tot);  // base-2 units
+  const float lse = lse2 * 0.69314718055994530942f;
+  const int64_t tgt = tokens[row + 1];
+  if (threadIdx.x == 0) {
+    const float xt = (tgt >= 0 && tgt < V) ? bf16_to_f32(x[tgt]) : NAN;
+    loss_rows[row] = lse - xt;
+    lse_out[row] = lse;
+  }
+#pragma unroll
+  for (int c = 0; c < kRC; ++c) {
+    const int64_t j = ((int64_t)c * kRT + threadIdx.x) * 8;
+    if (j >= full) continue;
+    u16x8_t o;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float g = exp2_hw(fmaf(bf16_to_f32(raw[c][t]), kLog2eX, -lse2)) - (j + t == tgt ? 1.f : 0.f);
+      o[t] = f32_to_bf16(g * inv_n);
+    }
+    *reinterpret_cast<u16x8_t*>(drow + j) = o;
+  }
+  if (jt < V) drow[jt] = f32_to_bf16((exp2_hw(fmaf(tail, kLog2eX, -lse2)) - (jt == tgt ? 1.f : 0.f)) * inv_n);
+  for (int64_t j = V + threadIdx.x; j < ld_d; j += kRT) drow[j] = f32_to_bf16(0.f);
+}
+
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kT) void xent_bwd_kernel(int S, int64_t V, const T* __restrict__ logits, int64_t ld,
                                                        const int64_t* __restrict__ tokens,
@@ -206,7 +288,10 @@ extern "C" int rh_xent_fwd(int dtype, int64_t batch, int64_t seq, int64_t vocab,
   const float inv_n = 1.0f / (float)(batch * (seq - 1));
   const bool vec = rh_aligned(logits, 16) && ld % 8 == 0 && (!dlogits || (rh_aligned(dlogits, 16) && ld_d % 8 == 0));
   if (dtype == RH_DTYPE_BF16) {
-    if (vec) hipLaunchKernelGGL((xent_fwd_kernel<bf16_t, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
+    if (vec && dlogits && vocab <= kRegCols)
+      hipLaunchKernelGGL(xent_fwd_grad_reg_kernel, dim3((unsigned)nrows), dim3(kRT), 0, st, (int)seq, vocab,
+                         (const bf16_t*)logits, ld, tokens, row_lse, rows, (bf16_t*)dlogits, ld_d, inv_n);
+    else if (vec) hipLaunchKernelGGL((xent_fwd_kernel<bf16_t, true>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
                                 (const bf16_t*)logits, ld, tokens, row_lse, rows, (bf16_t*)dlogits, ld_d, inv_n);
     else hipLaunchKernelGGL((xent_fwd_kernel<bf16_t, false>), dim3((unsigned)nrows), dim3(kT), 0, st, (int)seq, vocab,
                             (const bf16_t*)logits, ld, tokens, row_lse, rows, (bf16_t*)dlogits, ld_d, inv_n);

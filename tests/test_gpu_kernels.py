@@ -320,6 +320,25 @@ def test_next_token_loss(cuda, dtype, batch, seq, vocab):
     assert torch.all(logits.grad[:, -1] == 0)
 
 
+@pytest.mark.parametrize("batch,seq,vocab,ld", [(2, 64, 50257, 50264), (3, 5, 13, 16), (2, 4, 65536, 65536)])
+def test_next_token_loss_padded_bf16_rows(cuda, batch, seq, vocab, ld):
+    """bf16 logits whose rows start 16-byte aligned (row stride a multiple of 8, as the LM head lays
+    them out): the fused forward keeps each row in registers; vocab not a multiple of 8 exercises
+    the tail columns."""
+    buf = _rand(batch, seq, ld, dtype=torch.bfloat16, seed=42, scale=3.0)
+    logits = buf[..., :vocab].requires_grad_(True)
+    g = torch.Generator().manual_seed(43)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g).to(cuda)
+    loss = ops.next_token_loss(logits, tokens, vocab)
+    lr = logits.detach().float().requires_grad_(True)
+    ref = torch_ref.next_token_loss(lr, tokens, vocab)
+    assert abs(float(loss) - float(ref)) <= 1e-3 * max(1.0, abs(float(ref)))
+    loss.backward()
+    ref.backward()
+    assert rel_inf(logits.grad, lr.grad) <= BF16_TOL
+    assert torch.all(logits.grad[:, -1] == 0)
+
+
 def test_next_token_loss_of_zero_logits_is_log_vocab(cuda):
     logits = torch.zeros(2, 16, 1000, device=cuda)
     tokens = torch.randint(0, 1000, (2, 16), device=cuda)
