@@ -871,13 +871,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
 #pragma unroll
     for (int i = 0; i < KS; ++i) asm volatile("" ::"v"(qreg[i]), "v"(doreg[i]));
     __syncthreads();
-    for (int t = 0; t < nst; ++t) {
+    // One stage in LDS slot `slot` (= t & 1, a compile-time constant: every fragment address of the
+    // stage is a per-lane base plus an instruction immediate).
+    auto stage = [&](int t, auto slot) {
+      constexpr int cur = decltype(slot)::value;
       if (t + 1 < nst) {
-        const uint32_t nxt = s0 + (uint32_t)(((t + 1) & 1) * 4 * TILE);
+        const uint32_t nxt = s0 + (uint32_t)((cur ^ 1) * 4 * TILE);
         kvdma.issue(nxt, kbase, (t + 1) * kStageRows, S - 1, w, lane);
         kvdma.issue(nxt + 2 * TILE, vbase, (t + 1) * kStageRows, S - 1, w, lane);
       }
-      const bf16_t* sK = smem + (t & 1) * 2 * TILE;
+      const bf16_t* sK = smem + cur * 2 * TILE;
       const bf16_t* sV = sK + TILE;
       const int kt0 = t * kStageRows + 32 * ph;
       if (wq0 < S && kt0 < kv_end && !(a.causal && kt0 > wq1)) {
@@ -887,19 +890,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
           st = mfma32(row_frag<D>(sK, 32 * ph, i, fa), qreg[i], st);
           dpt = mfma32(row_frag<D>(sV, 32 * ph, i, fa), doreg[i], dpt);
         }
+        // masked scores become -inf (p = 0, dS = 0) and every stage runs one straight-line body
         if ((a.causal && kt0 + 31 > wq0) || kt0 + 31 >= S || wq1 >= S) {  // diagonal or ragged stage
           const bool diag = a.causal && kt0 + 31 > wq0;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            const bool ok = qok && key < S && !(diag && key > q_row);
-            const float p = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) : 0.f;
-            st[r] = p * (dpt[r] - del);
+            if (!(qok && key < S && !(diag && key > q_row))) st[r] = -INFINITY;
           }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) st[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - del);
         }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - del);
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t dsb = pack8(st, s2);
@@ -909,7 +910,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_mfma(AttnArgs<bf16_t> a, int 
       }
       wait_vm();
       __syncthreads();
+    };
+    int t = 0;
+    for (; t + 1 < nst; t += 2) {
+      stage(t, std::integral_constant<int, 0>{});
+      stage(t + 1, std::integral_constant<int, 1>{});
     }
+    if (t < nst) stage(t, std::integral_constant<int, 0>{});
     merge_phases<0, DB>(cbuf, dqt, w, lane);
     if (ph == 0 && qok) {
       bf16_t* dqp = a.dq + (tok0 + q_row) * a.ld_d + (int64_t)h * D;
