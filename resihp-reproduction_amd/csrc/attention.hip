@@ -450,8 +450,8 @@ struct RowDma {
     const int row = wave * RPW + lane / CPR;
     off = (uint32_t)(2 * (int64_t)(lane / CPR) * ld + 16 * sw_chunk(row, lane % CPR));
   }
-  // The same load with the tile given as an LDS byte address; the stage's first row of this
-  // wave is formed once and each further window is a fixed byte stride from it.
+  // The load, with the tile given as an LDS byte address: the stage's first row of this wave is
+  // formed once and each further window is a fixed byte stride from it.
   __device__ __forceinline__ void issue(uint32_t tile, const bf16_t* base, int r0, int last, int wave,
                                         int lane) const {
     if (r0 + ROWS - 1 <= last) {
@@ -466,22 +466,6 @@ struct RowDma {
         const int grow = max(min(row, last - r0), 0);
         dma16s(sb, (uint32_t)(2 * (int64_t)grow * ld + 16 * sw_chunk(row, lane % CPR)),
                tile + (uint32_t)((wave + 8 * i) * 1024));
-      }
-    }
-  }
-  __device__ __forceinline__ void issue(bf16_t* tile, const bf16_t* base, int r0, int last, int wave,
-                                        int lane) const {
-    if (r0 + ROWS - 1 <= last) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i)
-        dma16s(base + (int64_t)(r0 + (wave + 8 * i) * RPW) * ld, off, tile + (wave + 8 * i) * 512);
-    } else {
-      const bf16_t* sb = base + (int64_t)r0 * ld;
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int row = (wave + 8 * i) * RPW + lane / CPR;
-        const int grow = max(min(row, last - r0), 0);
-        dma16s(sb, (uint32_t)(2 * (int64_t)grow * ld + 16 * sw_chunk(row, lane % CPR)), tile + (wave + 8 * i) * 512);
       }
     }
   }

@@ -137,19 +137,8 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
 // compiler cannot see that the asynchronous LDS write never aliases the stages being read, and
 // with the builtin it waits for every outstanding load before each LDS read, serialising the
 // pipeline.  Completion is tracked explicitly with wait_vm_le (these loads count in vmcnt).
-__device__ __forceinline__ void dma16(const bf16_t* src, const bf16_t* lds_dst) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "s"(lds)
-      : "memory", "m0");
-}
-
-// The same with the LDS destination given as a wave-uniform 32-bit LDS byte address.
+// The LDS destination is a wave-uniform 32-bit LDS byte address: a generic-to-LDS pointer
+// conversion per load would cost a null check in scalar instructions.
 __device__ __forceinline__ void dma16(const bf16_t* src, uint32_t lds_dst) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
@@ -163,28 +152,11 @@ __device__ __forceinline__ void dma16(const bf16_t* src, uint32_t lds_dst) {
 // The same load in saddr form: lane l fetches the 16 bytes at sbase + voff (sbase wave-uniform,
 // held in SGPRs; voff a 32-bit per-lane byte offset), so a stage of loads needs one 32-bit
 // offset register per load instead of a 64-bit pointer.
-__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, const bf16_t* lds_dst) {
-  // (readfirstlane returns a signed int: widen through uint32_t, never by sign extension)
-  const uint64_t b = (uint64_t)(uintptr_t)sbase;
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
-  // s_nop 4: five wait states, so an SGPR base written by a VALU op (readfirstlane) just
-  // before this statement is settled when the load reads it (the M0 write needs one)
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 4\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(sb), "s"(lds)
-      : "memory", "m0");
-}
-
-// dma16s with the LDS destination given as a byte address (wave-uniform): callers that keep their
-// tiles as LDS addresses avoid the generic-to-LDS pointer conversion and its null check.
+// (the LDS destination is a wave-uniform byte address, as for dma16; s_nop 4: five wait states, so an
+// SGPR base written by a VALU op (readfirstlane) just before this statement is settled when the
+// load reads it, the M0 write needs one)
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  // (readfirstlane returns a signed int: widen through uint32_t, never by sign extension)
   const uint64_t b = (uint64_t)(uintptr_t)sbase;
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);

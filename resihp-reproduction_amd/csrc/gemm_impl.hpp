@@ -904,19 +904,11 @@ struct DmaOperand {
       }
     }
   }
-  __device__ __forceinline__ void issue(bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) issue_one(i, dst, kt, krow0, wave);
-  }
+  // dst: the tile as a 32-bit LDS byte address (wave-uniform, scalar math)
   __device__ __forceinline__ void issue(uint32_t dst, int kt, const bf16_t* krow0, int wave) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) issue_one(i, dst, kt, krow0, wave);
   }
-  __device__ __forceinline__ void issue_one(int i, bf16_t* dst, int kt, const bf16_t* krow0, int wave) {
-    const int win = wave + NWAVES * i;
-    dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + win * 512);
-  }
-  // the same with the LDS destination as a 32-bit LDS byte address (wave-uniform, scalar math)
   __device__ __forceinline__ void issue_one(int i, uint32_t dst, int kt, const bf16_t* krow0, int wave) {
     const int win = wave + NWAVES * i;
     dma16(KC ? rowp[i] + (int64_t)kt * kBK : krow0 + off[i], dst + (uint32_t)win * 1024u);
